@@ -1,0 +1,225 @@
+#!/usr/bin/env python
+"""Headline benchmark: INT4 W4A16 GEMV 4096x4096, streaming (HBM-cold), on
+one MI355X.  Prints ONE JSON line (the driver's contract).
+
+A step is one GEMV call on one set of inputs.  Streaming mode rotates
+through a pool of distinct (W_packed, scale, x, y) sets totalling more than
+512 MiB, so W is read from HBM on every call (the 256 MB MALL cannot hold
+the pool).  The timed loop runs in native code (cq_pool_timing): K launches
+back to back on one stream, each dispatch carrying its own start/stop
+events, between a barrier + torch.cuda.synchronize() on both sides.
+
+  value      algorithmic bytes x K / event time of the whole timed loop
+             (GB/s, whole-job throughput, inputs resident in HBM)
+  roofline   the kernel: algorithmic bytes per launch / mean device
+             duration of the K launches (from their own events), against
+             8 TB/s; `traffic` is the profiled HBM bytes per launch from
+             the committed rocprofv3 counter summary, when present
+  cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
+             on the same shape, median of 20 calls, timed on this host
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+BASELINE = json.loads((ROOT / "BASELINE.json").read_text())
+METRIC = BASELINE["metric"]
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "int4gemv_4096x4096_streaming_traffic.json"
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--variant", default="int4gemv_cdna4")
+    ap.add_argument("--n", type=int, default=4096)
+    ap.add_argument("--k", type=int, default=4096)
+    ap.add_argument("--mode", choices=("streaming", "hot"), default="streaming")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--no-detail", action="store_true",
+                    help="skip the INT8 / hot-mode detail measurements")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB "
+                         "(counter calibration runs)")
+    return ap.parse_args(argv)
+
+
+def gpu_loop(op: str, variant: str, sets, steps: int, warmup: int) -> dict:
+    import torch
+    from cudalab_amd.ext import pool_timing
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
+                    per_kernel=True)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    ku = r["kernel_us"]
+    return {"total_us": r["total_us"], "wall_s": wall_s,
+            "kernel_mean_us": statistics.fmean(ku),
+            "kernel_median_us": statistics.median(ku),
+            "kernel_min_us": min(ku)}
+
+
+def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
+    from cudalab_amd.evaluator.bench import cold_pool_sets
+    if op == "int4gemv":
+        from cudalab_amd.operators.int4gemv import device_random_set, int4_bytes
+        nbytes = int4_bytes(N, K)
+    else:
+        from cudalab_amd.operators.qgemv import device_random_set, q8_bytes
+        nbytes = q8_bytes(N, K)
+    n = cold_pool_sets(nbytes) if mode == "streaming" else 1
+    return [device_random_set(N, K, seed + 100000 + i) for i in range(n)], nbytes
+
+
+def cpu_baseline(N: int, K: int, sets) -> dict:
+    """Oracle CPU GEMV on one set's inputs copied to host (untimed copy)."""
+    import numpy as np
+    from oracle import oracle as orc
+    wp, s, x, _ = sets[0]
+    wpn = wp.cpu().numpy()
+    sn = s.cpu().numpy()
+    xn = x.cpu().numpy()
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or min(16, os.cpu_count() or 1)
+    for _ in range(3):
+        orc.gemv_w4_cpu(wpn, sn, xn, threads)
+    times = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        y = orc.gemv_w4_cpu(wpn, sn, xn, threads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    from cudalab_amd.operators.int4gemv import int4_bytes
+    ex, S = orc.exact_w4(wpn, sn, xn)
+    assert orc.arith_ratio(y, ex, S, K).max() <= 1.0
+    return {"value": round(int4_bytes(N, K) / med / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"20 calls (after 3 warmup) of the INT4 {N}x{K} GEMV "
+                      f"on one input set, median {med * 1e6:.1f} us; fused "
+                      f"unpack-dequant-dot in C + OpenMP",
+            "us_per_call": round(med * 1e6, 2)}
+
+
+def load_traffic(N: int, K: int):
+    if not TRAFFIC_FILE.exists():
+        return None
+    try:
+        d = json.loads(TRAFFIC_FILE.read_text())
+        if d.get("shape") == [N, K]:
+            return d.get("hbm_bytes_per_launch")
+    except Exception:  # noqa: BLE001
+        return None
+    return None
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is "
+              "not supported (the sharded design is described in DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import torch
+    from cudalab_amd.build import build
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    ext4 = build("int4gemv")
+    N, K = args.n, args.k
+    sets, nbytes = make_sets("int4gemv", N, K, args.mode)
+    for (wp, s, x, out) in sets[:1]:
+        ext4.forward_into(args.variant, wp, s, x, out)   # validate once
+    plan = ext4.describe(args.variant, sets[0][0], sets[0][2])
+
+    if args.calib_copy_mib:
+        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8,
+                          device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    torch.cuda.synchronize()           # barrier (one rank) + sync
+    r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup)
+    torch.cuda.synchronize()
+
+    total_s = r["total_us"] * 1e-6
+    value = nbytes * args.steps / total_s / 1e9
+    achieved = nbytes / (r["kernel_mean_us"] * 1e-6) / 1e9
+    traffic = load_traffic(N, K)
+
+    detail = {"plan": plan, "pool_sets": len(sets),
+              "pool_bytes": len(sets) * nbytes,
+              "us_per_call_loop": round(r["total_us"] / args.steps, 4),
+              "kernel_us_mean": round(r["kernel_mean_us"], 4),
+              "kernel_us_median": round(r["kernel_median_us"], 4),
+              "kernel_us_min": round(r["kernel_min_us"], 4),
+              "wall_s_timed": round(r["wall_s"], 4)}
+    if not args.no_detail:
+        hot_sets = sets[:1]
+        h = gpu_loop("int4gemv", args.variant, hot_sets, 2000, 200)
+        detail["hot_kernel_us_mean"] = round(h["kernel_mean_us"], 4)
+        detail["hot_us_per_call_loop"] = round(h["total_us"] / 2000, 4)
+        build("qgemv")
+        q_sets, q_bytes = make_sets("qgemv", N, K, args.mode)
+        q = gpu_loop("qgemv", "qgemv_cdna4", q_sets, 2000, 200)
+        detail["int8_kernel_us_mean"] = round(q["kernel_mean_us"], 4)
+        detail["int8_us_per_call_loop"] = round(q["total_us"] / 2000, 4)
+        detail["int8_GBps_kernel"] = round(q_bytes / q["kernel_mean_us"] / 1e3, 1)
+        detail["speedup_int4_vs_int8_kernel"] = round(
+            q["kernel_mean_us"] / r["kernel_mean_us"], 3)
+        detail["speedup_int4_vs_int8_loop"] = round(
+            (q["total_us"] / 2000) / (r["total_us"] / args.steps), 3)
+        del q_sets
+        torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu:
+        cpu_sets, _ = make_sets("int4gemv", N, K, "hot")
+        cpu = cpu_baseline(N, K, cpu_sets)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_s * 1e3 / args.steps, 6),
+        "us_per_call": round(r["total_us"] / args.steps, 4),
+        "kernel_us_per_call": round(r["kernel_mean_us"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic: W ~ N(0,0.02) fp16 quantized G=128, x ~ N(0,1) "
+                "fp16, drawn on the device",
+        "config": {"workload": f"INT4 W4A16 GEMV {N}x{K} {args.mode} "
+                               f"({'HBM-cold pool of %d distinct sets' % detail['pool_sets'] if args.mode == 'streaming' else 'single resident set'})",
+                   "N": N, "K": K, "group_size": 128,
+                   "variant": args.variant, "mode": args.mode,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,164 @@
+"""ctypes binding of `libcdnaqgemv.so` (declarations in include/cdnaqgemv.h).
+
+Loading happens once, on first use.  There is no fallback: if the library
+is missing or does not export the declared symbols, every entry point
+raises, so no GEMV can silently run anywhere but in the HIP kernels.
+
+The library must be loaded after `import torch` so that its HIP runtime
+dependency (soname libamdhip64.so.7) binds to the runtime torch already
+loaded: streams and device pointers handed over from torch are then valid
+in the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from .build import LIB_PATH
+
+CQ_OK = 0
+CQ_ERR_UNKNOWN_VARIANT = 1
+CQ_ERR_INVALID_ARG = 2
+CQ_ERR_HIP = 3
+CQ_ERR_BUFFER_TOO_SMALL = 4
+
+CQ_OP_INT4GEMV = 0
+CQ_OP_QGEMV = 1
+
+CQ_LIST_NORMAL = 0
+CQ_LIST_ALL = 1
+CQ_LIST_QUARANTINED = 2
+CQ_LIST_ALIASES = 3
+
+OPS = {"int4gemv": CQ_OP_INT4GEMV, "qgemv": CQ_OP_QGEMV}
+
+
+class CqTiming(ctypes.Structure):
+    _fields_ = [
+        ("warmup", ctypes.c_int64),
+        ("n_windows", ctypes.c_int64),
+        ("launches_per_window", ctypes.c_int64),
+        ("median_us", ctypes.c_double),
+        ("min_us", ctypes.c_double),
+        ("max_us", ctypes.c_double),
+        ("mean_us", ctypes.c_double),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_cstr = ctypes.c_char_p
+
+# name -> (restype, argtypes); must match include/cdnaqgemv.h
+SIGNATURES = {
+    "cq_int4gemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "cq_qgemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "cq_native_timing": (ctypes.c_int, [
+        ctypes.c_int, _cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
+        _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(CqTiming)]),
+    "cq_pool_timing": (ctypes.c_int, [
+        ctypes.c_int, _cstr, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+        ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64, _i64, _i64, _vp,
+        _i64, _i64, ctypes.POINTER(ctypes.c_float),
+        ctypes.POINTER(ctypes.c_double)]),
+    "cq_variants": (ctypes.c_int, [ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_char_p, ctypes.c_size_t]),
+    "cq_vec_contract_ok": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64]),
+    "cq_describe_launch": (ctypes.c_int, [ctypes.c_int, _cstr, _i64, _i64,
+                                          _vp, _vp, ctypes.c_char_p,
+                                          ctypes.c_size_t]),
+    "cq_last_error": (ctypes.c_char_p, []),
+    "cq_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib_path() -> Path:
+    return LIB_PATH
+
+
+def load():
+    """Load the library once and declare every signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (bind libamdhip64 to torch's runtime first)
+        if not LIB_PATH.exists():
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m cudalab_amd.build` "
+                "(or __graft_entry__.build()). The HIP library is the only "
+                "implementation of this path: there is no CPU fallback.")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)  # AttributeError if not exported
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().cq_last_error().decode("utf-8", "replace")
+
+
+def check(status: int, what: str) -> None:
+    if status != CQ_OK:
+        raise RuntimeError(f"{what} failed (status {status}): {last_error()}")
+
+
+def _string_call(fn, *args) -> str:
+    need = fn(*args, None, 0)
+    if need < 0:
+        raise RuntimeError(f"{fn.__name__} failed (status {need}): "
+                           f"{last_error()}")
+    buf = ctypes.create_string_buffer(need)
+    got = fn(*args, buf, need)
+    if got != need:
+        raise RuntimeError(f"{fn.__name__}: size changed ({need} -> {got})")
+    return buf.value.decode("utf-8")
+
+
+def variant_list(op: str, which: int = CQ_LIST_NORMAL) -> list[str]:
+    s = _string_call(load().cq_variants, OPS[op], which)
+    return [v for v in s.split("\n") if v]
+
+
+def aliases(op: str) -> dict[str, str]:
+    out = {}
+    for line in variant_list(op, CQ_LIST_ALIASES):
+        a, t = line.split("=", 1)
+        out[a] = t
+    return out
+
+
+def describe_launch(op: str, variant: str, n: int, k: int, w_ptr: int,
+                    x_ptr: int) -> dict:
+    s = _string_call(load().cq_describe_launch, OPS[op],
+                     variant.encode(), n, k, w_ptr, x_ptr)
+    return parse_launch_line(s)
+
+
+def parse_launch_line(s: str) -> dict:
+    """Parse cq_describe_launch's "key=value ... why=<free text>" line."""
+    head, why = s.split(" why=", 1)
+    out = dict(tok.split("=", 1) for tok in head.split(" "))
+    out["why"] = why
+    return out
+
+
+def vec_contract_ok(op: str, w_ptr: int, x_ptr: int, k: int) -> bool:
+    return bool(load().cq_vec_contract_ok(OPS[op], w_ptr, x_ptr, k))
+
+
+def version() -> str:
+    return load().cq_version().decode()

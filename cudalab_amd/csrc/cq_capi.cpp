@@ -1,0 +1,363 @@
+// C ABI of libcdnaqgemv.so (declared in include/cdnaqgemv.h).
+//
+// The variant registry, the launch entry points and the two timing loops.
+// The registry is a constant table (no static-initialisation registrars):
+// names are unique by construction and lists are sorted on output, which is
+// the contract of the reference's registry
+// (kernels/int4gemv/bindings.cpp:41-56,136-142,258-285).
+//
+// Validation here is limited to what a safe launch needs.  Dtype,
+// contiguity, device and shape-consistency checks with the reference's
+// messages live in the Python layer (cudalab_amd/ext.py), which sees the
+// tensors; this layer sees only pointers and sizes.
+
+#include "cdnaqgemv.h"
+#include "cq_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cstdio>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+struct Variant {
+    const char* name;
+    int op;
+    int kind;         // cq::Kind
+    int rows;         // rows per lane; 0 = library default per shape
+    bool quarantined; // registered but hidden from the normal list
+};
+
+// Quarantine is kept as a mechanism (a variant can be listed here with
+// quarantined = true) and is empty today, as in the reference
+// (kernels/int4gemv/bindings.cpp:46-56).
+constexpr Variant kVariants[] = {
+    {"int4gemv_baseline", CQ_OP_INT4GEMV, cq::kScalar, 0, false},
+    {"int4gemv_cdna4", CQ_OP_INT4GEMV, cq::kWave, 0, false},
+    {"int4gemv_wave_r1", CQ_OP_INT4GEMV, cq::kWave, 1, false},
+    {"int4gemv_wave_r2", CQ_OP_INT4GEMV, cq::kWave, 2, false},
+    {"int4gemv_wave_r4", CQ_OP_INT4GEMV, cq::kWave, 4, false},
+    {"qgemv_baseline", CQ_OP_QGEMV, cq::kScalar, 0, false},
+    {"qgemv_cdna4", CQ_OP_QGEMV, cq::kWave, 0, false},
+    {"qgemv_wave_r1", CQ_OP_QGEMV, cq::kWave, 1, false},
+    {"qgemv_wave_r2", CQ_OP_QGEMV, cq::kWave, 2, false},
+    {"qgemv_wave_r4", CQ_OP_QGEMV, cq::kWave, 4, false},
+};
+
+// The reference's vectorized variant names, accepted so that callers with
+// a hard-coded name keep working (scripts/gen3_native_timing.py:59,66 uses
+// qgemv_vec16_row).  Every one of them had the same operator contract,
+// alignment contract and scalar fallback; they resolve to the CDNA4
+// incumbent of their operator.
+struct Alias {
+    const char* alias;
+    const char* target;
+    int op;
+};
+constexpr Alias kAliases[] = {
+    {"int4gemv_vec16_row", "int4gemv_cdna4", CQ_OP_INT4GEMV},
+    {"int4gemv_rowtile4", "int4gemv_cdna4", CQ_OP_INT4GEMV},
+    {"int4gemv_rowtile8", "int4gemv_cdna4", CQ_OP_INT4GEMV},
+    {"int4gemv_rowtile4_hx", "int4gemv_cdna4", CQ_OP_INT4GEMV},
+    {"qgemv_vec16_row", "qgemv_cdna4", CQ_OP_QGEMV},
+    {"qgemv_vec16_scale", "qgemv_cdna4", CQ_OP_QGEMV},
+    {"qgemv_warp_vec16", "qgemv_cdna4", CQ_OP_QGEMV},
+    {"qgemv_warp_vec16_ilp4", "qgemv_cdna4", CQ_OP_QGEMV},
+};
+
+const char* op_name(int op) {
+    return op == CQ_OP_INT4GEMV ? "int4gemv" : (op == CQ_OP_QGEMV ? "qgemv" : "?");
+}
+
+const Variant* find_variant(int op, const char* name) {
+    if (name == nullptr) return nullptr;
+    for (const Alias& a : kAliases)
+        if (a.op == op && std::strcmp(a.alias, name) == 0) name = a.target;
+    for (const Variant& v : kVariants)
+        if (v.op == op && std::strcmp(v.name, name) == 0) return &v;
+    return nullptr;
+}
+
+// Shared pre-launch checks of both operators.  Returns CQ_OK or a status
+// with the message set.
+int check_call(int op, const char* variant, const Variant** out,
+               const void* w, const void* scale, const void* x,
+               const void* y, int64_t n, int64_t k) {
+    if (op != CQ_OP_INT4GEMV && op != CQ_OP_QGEMV)
+        return fail(CQ_ERR_INVALID_ARG, "unknown operator id " + std::to_string(op));
+    if (variant == nullptr) return fail(CQ_ERR_INVALID_ARG, "variant name is NULL");
+    const Variant* v = find_variant(op, variant);
+    if (v == nullptr)
+        return fail(CQ_ERR_UNKNOWN_VARIANT,
+                    std::string("unknown ") + op_name(op) + " variant '" + variant + "'");
+    if (w == nullptr || scale == nullptr || x == nullptr || y == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null device pointer");
+    if (n <= 0 || n > INT_MAX)
+        return fail(CQ_ERR_INVALID_ARG, "n must be in [1, 2^31-1], got " + std::to_string(n));
+    if (k <= 0 || k > INT_MAX)
+        return fail(CQ_ERR_INVALID_ARG, "k must be in [1, 2^31-1], got " + std::to_string(k));
+    if (op == CQ_OP_INT4GEMV && k % 128 != 0)
+        return fail(CQ_ERR_INVALID_ARG,
+                    "k must be divisible by 128 (group_size=128), got " + std::to_string(k));
+    *out = v;
+    return CQ_OK;
+}
+
+cq::Plan make_plan(int op, const Variant& v, int64_t n, int64_t k,
+                   const void* w, const void* x) {
+    return op == CQ_OP_INT4GEMV ? cq::plan_int4(v.kind, v.rows, n, k, w, x)
+                                : cq::plan_q8(v.kind, v.rows, n, k, w, x);
+}
+
+hipError_t launch_plan(int op, const cq::Plan& p, const void* w,
+                       const void* scale, const void* x, void* y, int64_t n,
+                       int64_t k, hipStream_t stream, hipEvent_t ev0,
+                       hipEvent_t ev1) {
+    return op == CQ_OP_INT4GEMV
+               ? cq::launch_int4(p, w, scale, x, y, n, k, stream, ev0, ev1)
+               : cq::launch_q8(p, w, scale, x, y, n, k, stream, ev0, ev1);
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(CQ_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) +
+                                " (" + hipGetErrorString(e) + ")");
+}
+
+int run_one(int op, const char* variant, const void* w, const void* scale,
+            const void* x, void* y, int64_t n, int64_t k, void* stream) {
+    g_last_error.clear();
+    const Variant* v = nullptr;
+    const int st = check_call(op, variant, &v, w, scale, x, y, n, k);
+    if (st != CQ_OK) return st;
+    const cq::Plan p = make_plan(op, *v, n, k, w, x);
+    const hipError_t e = launch_plan(op, p, w, scale, x, y, n, k,
+                                     static_cast<hipStream_t>(stream), nullptr, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return CQ_OK;
+}
+
+std::string join_sorted(std::vector<std::string> names) {
+    std::sort(names.begin(), names.end());
+    std::string s;
+    for (size_t i = 0; i < names.size(); ++i) {
+        if (i) s += '\n';
+        s += names[i];
+    }
+    return s;
+}
+
+int write_out(const std::string& s, char* buf, size_t cap) {
+    const size_t need = s.size() + 1;
+    if (need > static_cast<size_t>(INT_MAX)) return fail(CQ_ERR_INVALID_ARG, "string too long");
+    if (buf != nullptr && cap >= need) std::memcpy(buf, s.c_str(), need);
+    return static_cast<int>(need);
+}
+
+// Event pair owned for the duration of a timing call.
+struct Events {
+    std::vector<hipEvent_t> ev;
+    ~Events() {
+        for (hipEvent_t e : ev)
+            if (e != nullptr) (void)hipEventDestroy(e);
+    }
+    hipError_t make(size_t count) {
+        ev.assign(count, nullptr);
+        for (auto& e : ev) {
+            const hipError_t r = hipEventCreate(&e);
+            if (r != hipSuccess) return r;
+        }
+        return hipSuccess;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
+                const void* x, void* y, int64_t n, int64_t k, void* stream) {
+    return run_one(CQ_OP_INT4GEMV, variant, w_packed, scale, x, y, n, k, stream);
+}
+
+int cq_qgemv(const char* variant, const void* w_q, const void* scale,
+             const void* x, void* y, int64_t n, int64_t k, void* stream) {
+    return run_one(CQ_OP_QGEMV, variant, w_q, scale, x, y, n, k, stream);
+}
+
+int cq_native_timing(int op, const char* variant, const void* w,
+                     const void* scale, const void* x, void* y, int64_t n,
+                     int64_t k, void* stream, int64_t warmup,
+                     int64_t n_windows, int64_t launches_per_window,
+                     double* window_us, cq_timing_t* out) {
+    g_last_error.clear();
+    if (warmup < 0) return fail(CQ_ERR_INVALID_ARG, "warmup must be >= 0");
+    if (n_windows < 1) return fail(CQ_ERR_INVALID_ARG, "n_windows must be >= 1");
+    if (launches_per_window < 1)
+        return fail(CQ_ERR_INVALID_ARG, "launches_per_window must be >= 1");
+    const Variant* v = nullptr;
+    int st = check_call(op, variant, &v, w, scale, x, y, n, k);
+    if (st != CQ_OK) return st;
+    const cq::Plan p = make_plan(op, *v, n, k, w, x);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    for (int64_t i = 0; i < warmup; ++i) {
+        const hipError_t e = launch_plan(op, p, w, scale, x, y, n, k, s, nullptr, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "warmup launch");
+    }
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+
+    Events evs;
+    if ((e = evs.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+    std::vector<double> per(static_cast<size_t>(n_windows));
+    for (int64_t wdx = 0; wdx < n_windows; ++wdx) {
+        if ((e = hipEventRecord(evs.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+        for (int64_t i = 0; i < launches_per_window; ++i) {
+            e = launch_plan(op, p, w, scale, x, y, n, k, s, nullptr, nullptr);
+            if (e != hipSuccess) return hip_fail(e, "timed launch");
+        }
+        if ((e = hipEventRecord(evs.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+        if ((e = hipEventSynchronize(evs.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        float ms = 0.f;
+        if ((e = hipEventElapsedTime(&ms, evs.ev[0], evs.ev[1])) != hipSuccess)
+            return hip_fail(e, "hipEventElapsedTime");
+        per[static_cast<size_t>(wdx)] =
+            static_cast<double>(ms) * 1e3 / static_cast<double>(launches_per_window);
+    }
+    if (window_us != nullptr) std::copy(per.begin(), per.end(), window_us);
+    if (out != nullptr) {
+        std::vector<double> srt = per;
+        std::sort(srt.begin(), srt.end());
+        const size_t m = srt.size();
+        out->warmup = warmup;
+        out->n_windows = n_windows;
+        out->launches_per_window = launches_per_window;
+        out->median_us = (m % 2 == 1) ? srt[m / 2] : 0.5 * (srt[m / 2 - 1] + srt[m / 2]);
+        out->min_us = srt.front();
+        out->max_us = srt.back();
+        out->mean_us = std::accumulate(srt.begin(), srt.end(), 0.0) / static_cast<double>(m);
+    }
+    return CQ_OK;
+}
+
+int cq_pool_timing(int op, const char* variant, const void* const* w,
+                   const void* const* scale, const void* const* x,
+                   void* const* y, int64_t n_sets, int64_t n, int64_t k,
+                   void* stream, int64_t warmup, int64_t n_launches,
+                   float* kernel_us, double* total_us) {
+    g_last_error.clear();
+    if (w == nullptr || scale == nullptr || x == nullptr || y == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null set array");
+    if (n_sets < 1) return fail(CQ_ERR_INVALID_ARG, "n_sets must be >= 1");
+    if (warmup < 0) return fail(CQ_ERR_INVALID_ARG, "warmup must be >= 0");
+    if (n_launches < 1) return fail(CQ_ERR_INVALID_ARG, "n_launches must be >= 1");
+    std::vector<cq::Plan> plans(static_cast<size_t>(n_sets));
+    const Variant* v = nullptr;
+    for (int64_t i = 0; i < n_sets; ++i) {
+        const int st = check_call(op, variant, &v, w[i], scale[i], x[i], y[i], n, k);
+        if (st != CQ_OK) return st;
+        plans[static_cast<size_t>(i)] = make_plan(op, *v, n, k, w[i], x[i]);
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto go = [&](int64_t i, hipEvent_t e0, hipEvent_t e1) {
+        const size_t si = static_cast<size_t>(i % n_sets);
+        return launch_plan(op, plans[si], w[si], scale[si], x[si], y[si], n, k, s, e0, e1);
+    };
+    hipError_t e;
+    for (int64_t i = 0; i < warmup; ++i)
+        if ((e = go(i, nullptr, nullptr)) != hipSuccess) return hip_fail(e, "warmup launch");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+
+    Events win;
+    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+    Events per;
+    if (kernel_us != nullptr &&
+        (e = per.make(2 * static_cast<size_t>(n_launches))) != hipSuccess)
+        return hip_fail(e, "hipEventCreate");
+    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    for (int64_t i = 0; i < n_launches; ++i) {
+        hipEvent_t e0 = kernel_us ? per.ev[2 * static_cast<size_t>(i)] : nullptr;
+        hipEvent_t e1 = kernel_us ? per.ev[2 * static_cast<size_t>(i) + 1] : nullptr;
+        if ((e = go(warmup + i, e0, e1)) != hipSuccess) return hip_fail(e, "timed launch");
+    }
+    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
+        return hip_fail(e, "hipEventElapsedTime");
+    if (total_us != nullptr) *total_us = static_cast<double>(ms) * 1e3;
+    if (kernel_us != nullptr) {
+        for (int64_t i = 0; i < n_launches; ++i) {
+            float kms = 0.f;
+            e = hipEventElapsedTime(&kms, per.ev[2 * static_cast<size_t>(i)],
+                                    per.ev[2 * static_cast<size_t>(i) + 1]);
+            if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime (kernel)");
+            kernel_us[i] = kms * 1e3f;
+        }
+    }
+    return CQ_OK;
+}
+
+int cq_variants(int op, int which, char* buf, size_t cap) {
+    g_last_error.clear();
+    if (op != CQ_OP_INT4GEMV && op != CQ_OP_QGEMV)
+        return fail(-CQ_ERR_INVALID_ARG, "unknown operator id " + std::to_string(op));
+    std::vector<std::string> names;
+    if (which == CQ_LIST_ALIASES) {
+        for (const Alias& a : kAliases)
+            if (a.op == op) names.push_back(std::string(a.alias) + "=" + a.target);
+    } else if (which == CQ_LIST_NORMAL || which == CQ_LIST_ALL ||
+               which == CQ_LIST_QUARANTINED) {
+        for (const Variant& v : kVariants) {
+            if (v.op != op) continue;
+            if (which == CQ_LIST_NORMAL && v.quarantined) continue;
+            if (which == CQ_LIST_QUARANTINED && !v.quarantined) continue;
+            names.push_back(v.name);
+        }
+    } else {
+        return fail(-CQ_ERR_INVALID_ARG, "unknown list selector " + std::to_string(which));
+    }
+    return write_out(join_sorted(names), buf, cap);
+}
+
+int cq_vec_contract_ok(int op, const void* w, const void* x, int64_t k) {
+    if (op == CQ_OP_INT4GEMV) return cq::int4_contract_ok(w, x, k) ? 1 : 0;
+    if (op == CQ_OP_QGEMV) return cq::q8_contract_ok(w, x, k) ? 1 : 0;
+    return 0;
+}
+
+int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
+                       const void* w, const void* x, char* buf, size_t cap) {
+    g_last_error.clear();
+    const Variant* v = nullptr;
+    // describe with stand-in scale/y pointers: only w/x alignment matters
+    const int st = check_call(op, variant, &v, w, w, x, w, n, k);
+    if (st != CQ_OK) return -st;
+    const cq::Plan p = make_plan(op, *v, n, k, w, x);
+    char line[512];
+    std::snprintf(line, sizeof line,
+                  "variant=%s kernel=%s cw=%d j=%d r=%d block=%d grid=%lld fallback=%d why=%s",
+                  v->name, p.kind == cq::kScalar ? "scalar" : "wave", p.cw, p.j, p.r,
+                  p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
+                  p.why.empty() ? "-" : p.why.c_str());
+    return write_out(line, buf, cap);
+}
+
+const char* cq_last_error(void) { return g_last_error.c_str(); }
+
+const char* cq_version(void) { return "cdnaqgemv 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,54 @@
+// Internal interface between the C ABI layer (cq_capi.cpp) and the gfx950
+// kernels (cq_kernels.hip).  Not installed; the public surface is
+// include/cdnaqgemv.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+namespace cq {
+
+// Kernel families.  kScalar is the single scalar source shared by the
+// *_baseline variants and by every fallback, so a fallback is bit-identical
+// to the baseline on the same input.  kWave is the CDNA4 wave64 kernel.
+enum Kind : int { kScalar = 0, kWave = 1 };
+
+// Largest reduction length (elements) the wave kernels take; beyond it the
+// scalar kernel runs.  16384 = 8 register-resident x chunks per lane (INT4)
+// or 16 (INT8).
+constexpr int64_t kMaxWaveK = 16384;
+
+// A resolved launch: which kernel instance and with what shape.
+struct Plan {
+    int kind = kScalar;   // Kind
+    int cw = 0;           // lanes per row segment (16, 32 or 64)
+    int j = 0;            // chunks held per lane (x registers)
+    int r = 0;            // rows per lane
+    int block = 0;        // threads per workgroup
+    int64_t grid = 0;     // workgroups
+    bool fallback = false;  // requested a wave variant, got the scalar kernel
+    std::string why;      // reason for a fallback ("" otherwise)
+};
+
+// Launch-shape selection.  `rows` = 0 lets the library pick rows per lane
+// from its tuning table; otherwise it is the requested rows per lane
+// (clamped to what the register budget of the instance allows).
+Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
+               const void* x);
+Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
+             const void* x);
+
+bool int4_contract_ok(const void* w, const void* x, int64_t k);
+bool q8_contract_ok(const void* w, const void* x, int64_t k);
+
+// Enqueue one launch of `plan` on `stream`.  ev0/ev1, when non-null, are
+// attached to the dispatch itself (start/stop of the kernel).
+hipError_t launch_int4(const Plan& plan, const void* w, const void* scale,
+                       const void* x, void* y, int64_t n, int64_t k,
+                       hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
+hipError_t launch_q8(const Plan& plan, const void* w, const void* scale,
+                     const void* x, void* y, int64_t n, int64_t k,
+                     hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
+
+}  // namespace cq

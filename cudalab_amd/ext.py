@@ -1,0 +1,391 @@
+"""Python extension objects for the two operators, over the C ABI.
+
+Drop-in for the reference's per-operator pybind modules
+(kernels/int4gemv/bindings.cpp:287-316, kernels/qgemv/bindings.cpp:280-308):
+the same functions (`forward`, `forward_into`, `native_timing`, `variants`,
+`all_variants`, `quarantined_variants`), the same argument meaning, the same
+validation order, and the same message substrings, which callers match
+(cudalab/int4gemv_negative.py:108-318, cudalab/qgemv_negative.py:103-300).
+Every check runs on host metadata before anything is launched and raises
+RuntimeError (the type TORCH_CHECK surfaced as).
+
+What differs by design: validation lives here, in Python, where the CPU
+test suite can reach it; the C layer receives plain pointers and sizes and
+picks the kernel (vectorized or scalar fallback) from alignment.  Launches
+go on the current torch stream of the weights' device.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _capi
+
+NATIVE_TIMING_NOTE = (
+    "native kernel-loop caliber: back-to-back launches from C++ between two "
+    "HIP events on the current stream, window time / launches; no Python "
+    "boundary inside the window (distinct from the API-path caliber and from "
+    "the profiler's per-dispatch kernel duration)")
+
+
+def _fail(msg: str) -> None:
+    raise RuntimeError(msg)
+
+
+def _same_device(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.device == b.device
+
+
+class _OpExt:
+    """Common machinery; subclasses define the operator and its checks."""
+
+    op: str = ""
+
+    def __init__(self) -> None:
+        self._lib = _capi.load()
+        self._normal = _capi.variant_list(self.op, _capi.CQ_LIST_NORMAL)
+        self._all = _capi.variant_list(self.op, _capi.CQ_LIST_ALL)
+        self._quar = _capi.variant_list(self.op, _capi.CQ_LIST_QUARANTINED)
+        self._aliases = _capi.aliases(self.op)
+        self._fn = (self._lib.cq_int4gemv if self.op == "int4gemv"
+                    else self._lib.cq_qgemv)
+
+    # ---- registry (bindings.cpp variant lists) ----
+    def variants(self) -> list[str]:
+        """Dispatchable variants, sorted; quarantined ones excluded."""
+        return list(self._normal)
+
+    def all_variants(self) -> list[str]:
+        """Every registered variant, quarantined ones included, sorted."""
+        return list(self._all)
+
+    def quarantined_variants(self) -> list[str]:
+        return list(self._quar)
+
+    def aliases(self) -> dict[str, str]:
+        """Reference variant names accepted as aliases -> target variant."""
+        return dict(self._aliases)
+
+    def resolve(self, name: str) -> str:
+        return self._aliases.get(name, name)
+
+    def _unknown_variant_msg(self, name: str) -> str:
+        s = (f"未知 {self.op} 变体 '{name}'。正常可用: "
+             + " ".join(self._normal) + " ")
+        if self._quar:
+            s += ("；被隔离（NOT_FOR_NORMAL_DISPATCH）: " + " ".join(self._quar)
+                  + " （显式命名仍可调用，属受控历史审计入口）")
+        s += f"(unknown {self.op} variant)"
+        return s
+
+    def _lookup(self, name: str) -> str:
+        if not isinstance(name, str):
+            _fail(self._unknown_variant_msg(str(name)))
+        if name in self._all or name in self._aliases:
+            return name
+        _fail(self._unknown_variant_msg(name))
+
+    # ---- subclass hooks ----
+    def _validate_w(self, W: torch.Tensor) -> None:
+        raise NotImplementedError
+
+    def _validate_scale(self, W: torch.Tensor, scale: torch.Tensor) -> None:
+        raise NotImplementedError
+
+    def _validate_x(self, W: torch.Tensor, x: torch.Tensor) -> None:
+        raise NotImplementedError
+
+    def _k(self, W: torch.Tensor) -> int:
+        raise NotImplementedError
+
+    def _w_name(self) -> str:
+        raise NotImplementedError
+
+    def _validate_out(self, W: torch.Tensor, out: torch.Tensor) -> None:
+        if out.dim() != 1:
+            _fail(f"out 必须是 1 维 (N,)，实际 {out.dim()} 维 (out must be 1-D)")
+        if out.size(0) != W.size(0):
+            _fail(f"out 长度必须等于 N: out={out.size(0)} N={W.size(0)} "
+                  "(out length must equal N)")
+        if out.dtype != torch.float16:
+            _fail(f"out 必须是 float16，实际 {out.dtype} (out must be float16)")
+        if not out.is_contiguous():
+            _fail("out 必须是连续内存 (out must be contiguous)")
+        if not out.is_cuda:
+            _fail("out 必须是 CUDA 张量 (out must be a GPU tensor)")
+        if not _same_device(out, W):
+            _fail(f"out 必须与 {self._w_name()} 在同一 CUDA 设备上 "
+                  "(out must be on the weights' device)")
+
+    def _validate_inputs(self, W, scale, x) -> None:
+        self._validate_w(W)
+        self._validate_scale(W, scale)
+        self._validate_x(W, x)
+
+    # ---- launch ----
+    def _launch(self, variant: str, W, scale, x, out) -> None:
+        dev = W.device
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = self._fn(variant.encode(), W.data_ptr(), scale.data_ptr(),
+                          x.data_ptr(), out.data_ptr(), W.size(0), self._k(W),
+                          stream)
+        if st != _capi.CQ_OK:
+            _fail(f"{self.op} launch failed (status {st}): "
+                  f"{_capi.last_error()}")
+
+    def forward(self, variant: str, W: torch.Tensor, scale: torch.Tensor,
+                x: torch.Tensor) -> torch.Tensor:
+        """y = W_dequant @ x into a newly allocated fp16 (N,) tensor."""
+        self._lookup(variant)
+        self._validate_inputs(W, scale, x)
+        out = torch.empty(W.size(0), dtype=torch.float16, device=W.device)
+        self._launch(variant, W, scale, x, out)
+        return out
+
+    def forward_into(self, variant: str, W: torch.Tensor,
+                     scale: torch.Tensor, x: torch.Tensor,
+                     out: torch.Tensor) -> None:
+        """Same as forward, writing into a preallocated `out` (N,) fp16."""
+        self._lookup(variant)
+        self._validate_inputs(W, scale, x)
+        self._validate_out(W, out)
+        self._launch(variant, W, scale, x, out)
+
+    def native_timing(self, variant: str, W: torch.Tensor,
+                      scale: torch.Tensor, x: torch.Tensor,
+                      out: torch.Tensor, warmup: int = 200,
+                      n_windows: int = 10,
+                      launches_per_window: int = 64) -> dict:
+        """Native kernel-loop timing (bindings.cpp:180-253 semantics)."""
+        self._lookup(variant)
+        if warmup < 0:
+            _fail(f"warmup 必须 >= 0，实际 {warmup}")
+        if n_windows < 1:
+            _fail(f"n_windows 必须 >= 1，实际 {n_windows}")
+        if launches_per_window < 1:
+            _fail(f"launches_per_window 必须 >= 1，实际 {launches_per_window}")
+        self._validate_inputs(W, scale, x)
+        self._validate_out(W, out)
+        win = (ctypes.c_double * n_windows)()
+        res = _capi.CqTiming()
+        dev = W.device
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = self._lib.cq_native_timing(
+                _capi.OPS[self.op], variant.encode(), W.data_ptr(),
+                scale.data_ptr(), x.data_ptr(), out.data_ptr(), W.size(0),
+                self._k(W), stream, warmup, n_windows, launches_per_window,
+                win, ctypes.byref(res))
+        if st != _capi.CQ_OK:
+            _fail(f"native_timing failed (status {st}): {_capi.last_error()}")
+        return {
+            "variant": variant,
+            "warmup": int(warmup),
+            "n_windows": int(n_windows),
+            "launches_per_window": int(launches_per_window),
+            "window_median_us": [float(v) for v in win],
+            "median_us": res.median_us,
+            "min_us": res.min_us,
+            "max_us": res.max_us,
+            "mean_us": res.mean_us,
+            "note": NATIVE_TIMING_NOTE,
+        }
+
+    def describe(self, variant: str, W: torch.Tensor,
+                 x: torch.Tensor) -> dict:
+        """Kernel and launch shape the library would use (no launch)."""
+        self._lookup(variant)
+        s = _capi._string_call(self._lib.cq_describe_launch,
+                               _capi.OPS[self.op], variant.encode(),
+                               W.size(0), self._k(W), W.data_ptr(),
+                               x.data_ptr())
+        return _capi.parse_launch_line(s)
+
+    def contract_ok(self, W: torch.Tensor, x: torch.Tensor) -> bool:
+        """Host predicate of the vector contract for these tensors."""
+        return _capi.vec_contract_ok(self.op, W.data_ptr(), x.data_ptr(),
+                                     self._k(W))
+
+
+class Int4gemvExt(_OpExt):
+    """W4A16 INT4 GEMV: W_packed u8 (N,K/2), scale f16 (N,K/128), x f16 (K,).
+
+    Checks in the order of kernels/int4gemv/bindings.cpp:60-121."""
+
+    op = "int4gemv"
+
+    def _w_name(self) -> str:
+        return "W_packed"
+
+    def _k(self, W: torch.Tensor) -> int:
+        return 2 * W.size(1)
+
+    def _validate_w(self, Wp: torch.Tensor) -> None:
+        if Wp.dim() != 2:
+            _fail(f"W_packed 必须是 2 维 (N, K/2)，实际 {Wp.dim()} 维 "
+                  "(W_packed must be 2-D)")
+        if Wp.size(0) <= 0:
+            _fail(f"N 必须 > 0，实际 {Wp.size(0)} (N must be > 0)")
+        if Wp.size(1) <= 0:
+            _fail(f"K/2 必须 > 0，实际 {Wp.size(1)} (K/2 must be > 0)")
+        if Wp.dtype != torch.uint8:
+            _fail(f"W_packed 必须是 uint8，实际 {Wp.dtype} "
+                  "(W_packed must be uint8)")
+        K = 2 * Wp.size(1)
+        if K % 128 != 0:
+            _fail(f"K 必须可被 128 整除（group_size=128 合同）, 实际 K={K} "
+                  "(K must be divisible by 128)")
+        if not Wp.is_contiguous():
+            _fail("W_packed 必须是连续内存 (W_packed must be contiguous)")
+        if not Wp.is_cuda:
+            _fail("W_packed 必须是 CUDA 张量 (W_packed must be a GPU tensor)")
+
+    def _validate_scale(self, Wp: torch.Tensor, scale: torch.Tensor) -> None:
+        N, K = Wp.size(0), 2 * Wp.size(1)
+        if scale.dim() != 2:
+            _fail(f"scale 必须是 2 维 (N, K/128)，实际 {scale.dim()} 维 "
+                  "(scale must be 2-D)")
+        if scale.size(0) != N:
+            _fail(f"scale 行数必须等于 N: scale={scale.size(0)} N={N} "
+                  "(scale rows must equal N)")
+        if scale.size(1) != K // 128:
+            _fail(f"scale 组数必须等于 K/128（invalid group count）: "
+                  f"scale={scale.size(1)} K/128={K // 128}")
+        if scale.dtype != torch.float16:
+            _fail(f"scale 必须是 float16, 实际 {scale.dtype} "
+                  "(scale must be float16)")
+        if not scale.is_contiguous():
+            _fail("scale 必须是连续内存 (scale must be contiguous)")
+        if not scale.is_cuda:
+            _fail("scale 必须是 CUDA 张量 (scale must be a GPU tensor)")
+        if not _same_device(scale, Wp):
+            _fail("scale 必须与 W_packed 在同一 CUDA 设备上 "
+                  "(scale must be on W_packed's device)")
+
+    def _validate_x(self, Wp: torch.Tensor, x: torch.Tensor) -> None:
+        K = 2 * Wp.size(1)
+        if x.dim() != 1:
+            _fail(f"x 必须是 1 维 (K,)，实际 {x.dim()} 维 (x must be 1-D)")
+        if x.size(0) != K:
+            _fail(f"x 长度必须等于 K: x={x.size(0)} K={K} "
+                  "(x length must equal K)")
+        if x.dtype != torch.float16:
+            _fail(f"x 必须是 float16, 实际 {x.dtype} (x must be float16)")
+        if not x.is_contiguous():
+            _fail("x 必须是连续内存 (x must be contiguous)")
+        if not x.is_cuda:
+            _fail("x 必须是 CUDA 张量 (x must be a GPU tensor)")
+        if not _same_device(x, Wp):
+            _fail("x 必须与 W_packed 在同一 CUDA 设备上 "
+                  "(x must be on W_packed's device)")
+
+
+class QgemvExt(_OpExt):
+    """W8A16 INT8 GEMV: W_q i8 (N,K), scale f32 (N,), x f16 (K,).
+
+    Checks in the order of kernels/qgemv/bindings.cpp:65-121."""
+
+    op = "qgemv"
+
+    def _w_name(self) -> str:
+        return "W_q"
+
+    def _k(self, W: torch.Tensor) -> int:
+        return W.size(1)
+
+    def _validate_w(self, Wq: torch.Tensor) -> None:
+        if Wq.dim() != 2:
+            _fail(f"W_q 必须是 2 维 (N, K)，实际 {Wq.dim()} 维 (W_q must be 2-D)")
+        if Wq.size(0) <= 0:
+            _fail(f"N 必须 > 0，实际 {Wq.size(0)} (N must be > 0)")
+        if Wq.size(1) <= 0:
+            _fail(f"K 必须 > 0，实际 {Wq.size(1)} (K must be > 0)")
+        if Wq.dtype != torch.int8:
+            _fail(f"W_q 必须是 int8，实际 {Wq.dtype} (W_q must be int8)")
+        if not Wq.is_contiguous():
+            _fail("W_q 必须是连续内存 (W_q must be contiguous)")
+        if not Wq.is_cuda:
+            _fail("W_q 必须是 CUDA 张量 (W_q must be a GPU tensor)")
+
+    def _validate_scale(self, Wq: torch.Tensor, scale: torch.Tensor) -> None:
+        if scale.dim() != 1:
+            _fail(f"scale 必须是 1 维 (N,)，实际 {scale.dim()} 维 "
+                  "(scale must be 1-D)")
+        if scale.size(0) != Wq.size(0):
+            _fail(f"scale 长度必须等于 N: scale={scale.size(0)} N={Wq.size(0)} "
+                  "(scale length must equal N)")
+        if scale.dtype != torch.float32:
+            _fail(f"scale 必须是 float32，实际 {scale.dtype} "
+                  "(scale must be float32)")
+        if not scale.is_contiguous():
+            _fail("scale 必须是连续内存 (scale must be contiguous)")
+        if not scale.is_cuda:
+            _fail("scale 必须是 CUDA 张量 (scale must be a GPU tensor)")
+        if not _same_device(scale, Wq):
+            _fail("scale 必须与 W_q 在同一 CUDA 设备上 "
+                  "(scale must be on W_q's device)")
+
+    def _validate_x(self, Wq: torch.Tensor, x: torch.Tensor) -> None:
+        if x.dim() != 1:
+            _fail(f"x 必须是 1 维 (K,)，实际 {x.dim()} 维 (x must be 1-D)")
+        if x.size(0) != Wq.size(1):
+            _fail(f"x 长度必须等于 K: x={x.size(0)} K={Wq.size(1)} "
+                  "(x length must equal K)")
+        if x.dtype != torch.float16:
+            _fail(f"x 必须是 float16, 实际 {x.dtype} (x must be float16)")
+        if not x.is_contiguous():
+            _fail("x 必须是连续内存 (x must be contiguous)")
+        if not x.is_cuda:
+            _fail("x 必须是 CUDA 张量 (x must be a GPU tensor)")
+        if not _same_device(x, Wq):
+            _fail("x 必须与 W_q 在同一 CUDA 设备上 "
+                  "(x must be on W_q's device)")
+
+
+_EXTS: dict[str, _OpExt] = {}
+
+
+def get_ext(op: str) -> _OpExt:
+    """Singleton extension object for "int4gemv" or "qgemv"."""
+    if op not in ("int4gemv", "qgemv"):
+        raise KeyError(f"no extension for operator {op!r}")
+    e = _EXTS.get(op)
+    if e is None:
+        e = Int4gemvExt() if op == "int4gemv" else QgemvExt()
+        _EXTS[op] = e
+    return e
+
+
+def pool_timing(op: str, variant: str, sets: list, warmup: int,
+                n_launches: int, per_kernel: bool,
+                stream: Optional[torch.cuda.Stream] = None) -> dict:
+    """Rotating-pool launch loop in native code (cq_pool_timing).
+
+    `sets` is a list of (W, scale, x, out) tuples of one shape, already
+    validated by the caller.  Returns {"total_us": window event time,
+    "kernel_us": per-launch device durations (list) or None}."""
+    lib = _capi.load()
+    n = len(sets)
+    VP = ctypes.c_void_p * n
+    w = VP(*[s[0].data_ptr() for s in sets])
+    sc = VP(*[s[1].data_ptr() for s in sets])
+    xs = VP(*[s[2].data_ptr() for s in sets])
+    ys = VP(*[s[3].data_ptr() for s in sets])
+    W0 = sets[0][0]
+    N = W0.size(0)
+    K = 2 * W0.size(1) if op == "int4gemv" else W0.size(1)
+    ku = (ctypes.c_float * n_launches)() if per_kernel else None
+    tot = ctypes.c_double(0.0)
+    dev = W0.device
+    with torch.cuda.device(dev):
+        s = stream if stream is not None else torch.cuda.current_stream(dev)
+        st = lib.cq_pool_timing(
+            _capi.OPS[op], variant.encode(), w, sc, xs, ys, n, N, K,
+            s.cuda_stream, warmup, n_launches, ku, ctypes.byref(tot))
+    if st != _capi.CQ_OK:
+        _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")
+    return {"total_us": tot.value,
+            "kernel_us": [float(v) for v in ku] if ku is not None else None}

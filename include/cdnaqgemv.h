@@ -1,0 +1,177 @@
+/*
+ * cdnaqgemv.h — C ABI of the MI355X (gfx950) weight-only quantized GEMV
+ * library `libcdnaqgemv.so`.
+ *
+ * Two operators, both y[n] = sum_k Wdequant[n,k] * x[k] with FP32
+ * accumulation and one round-to-nearest-even cast to fp16 at the end:
+ *
+ *   int4gemv (W4A16, group-wise INT4):
+ *     w_packed u8 [n, k/2]  row-major; byte b of a row holds element 2b in
+ *                           its low nibble and element 2b+1 in its high
+ *                           nibble, 4-bit two's complement (-8..7)
+ *     scale    f16 [n, k/128]  one scale per group of 128 elements
+ *     x        f16 [k]
+ *     y        f16 [n]
+ *     Wdequant[n,k] = q[n,k] * float(scale[n, k/128]); k % 128 == 0.
+ *
+ *   qgemv (W8A16, per-row INT8):
+ *     w_q   i8  [n, k] row-major
+ *     scale f32 [n]
+ *     x     f16 [k]
+ *     y     f16 [n]
+ *     Wdequant[n,k] = w_q[n,k] * scale[n]; any k >= 1.
+ *
+ * All pointers are device pointers on the current HIP device; `stream` is a
+ * hipStream_t (NULL = the null stream).  Calls are asynchronous: a kernel is
+ * enqueued and the call returns.  The library never allocates device memory
+ * on these paths and keeps no state between calls.
+ *
+ * Vector contract (checked on the host before every launch): the vectorized
+ * kernels need w and x 16-byte aligned and k % 32 == 0 (int4gemv) or
+ * k % 16 == 0 (qgemv).  Inputs that miss it are never rejected: they run on
+ * the scalar kernel of the `*_baseline` variant, so their output is
+ * bit-identical to that variant's.
+ *
+ * Errors: every entry point returns a CQ_* status; on error nothing was
+ * launched (or, for CQ_ERR_HIP, the HIP runtime refused the launch) and
+ * cq_last_error() returns a message for the calling thread.  Metadata
+ * validation with the reference's messages (dtype, contiguity, device) is
+ * the Python layer's job; this layer re-checks only what it needs to launch
+ * safely (non-null pointers, positive sizes, k % 128 for int4gemv).
+ */
+#ifndef CDNAQGEMV_H
+#define CDNAQGEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define CQ_OK                   0
+#define CQ_ERR_UNKNOWN_VARIANT  1
+#define CQ_ERR_INVALID_ARG      2
+#define CQ_ERR_HIP              3
+#define CQ_ERR_BUFFER_TOO_SMALL 4
+
+/* operator ids */
+#define CQ_OP_INT4GEMV 0
+#define CQ_OP_QGEMV    1
+
+/* variant list selectors */
+#define CQ_LIST_NORMAL      0
+#define CQ_LIST_ALL         1
+#define CQ_LIST_QUARANTINED 2
+#define CQ_LIST_ALIASES     3
+
+/*
+ * One INT4 W4A16 GEMV launch: y = (unpack(w_packed) * scale) @ x.
+ * Replaces the variant entry `int4gemv_fn_t`
+ * (kernels/int4gemv/int4gemv_common.h:89-92) behind
+ * `int4gemv_forward` / `int4gemv_forward_into`
+ * (kernels/int4gemv/bindings.cpp:145-176).  `variant` is a name from
+ * cq_variants(CQ_OP_INT4GEMV, ...), e.g. "int4gemv_baseline".
+ */
+int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
+                const void* x, void* y, int64_t n, int64_t k, void* stream);
+
+/*
+ * One INT8 W8A16 GEMV launch: y = (w_q * scale[:,None]) @ x.
+ * Replaces `qgemv_fn_t` (kernels/qgemv/qgemv_common.h:64-67) behind
+ * `qgemv_forward` / `qgemv_forward_into`
+ * (kernels/qgemv/bindings.cpp:140-173).
+ */
+int cq_qgemv(const char* variant, const void* w_q, const void* scale,
+             const void* x, void* y, int64_t n, int64_t k, void* stream);
+
+/* Result of cq_native_timing; all times are per launch, microseconds. */
+typedef struct cq_timing {
+    int64_t warmup;
+    int64_t n_windows;
+    int64_t launches_per_window;
+    double median_us;
+    double min_us;
+    double max_us;
+    double mean_us;
+} cq_timing_t;
+
+/*
+ * Native kernel-loop timing: `warmup` untimed launches, then `n_windows`
+ * windows of `launches_per_window` back-to-back launches, each window
+ * bracketed by HIP events on `stream`; window_us[i] (caller-owned, length
+ * n_windows, may be NULL) receives window time / launches.  Replaces
+ * `int4gemv_native_timing` (kernels/int4gemv/bindings.cpp:180-253) and
+ * `qgemv_native_timing` (kernels/qgemv/bindings.cpp:175-249).  Synchronizes
+ * the stream.
+ */
+int cq_native_timing(int op, const char* variant, const void* w,
+                     const void* scale, const void* x, void* y, int64_t n,
+                     int64_t k, void* stream, int64_t warmup,
+                     int64_t n_windows, int64_t launches_per_window,
+                     double* window_us, cq_timing_t* out);
+
+/*
+ * Rotating-pool timing for HBM-cold ("streaming") measurement: launch i
+ * (0 <= i < warmup + n_launches) uses set (i % n_sets) of the caller's
+ * arrays w[], scale[], x[], y[].  For each of the n_launches timed launches
+ * kernel_us[i] (caller-owned, may be NULL) receives the kernel's own device
+ * duration from start/stop events attached to the dispatch
+ * (hipExtLaunchKernel), and *total_us the event time of the whole timed
+ * window.  No counterpart in the reference's C++ layer: it restates the
+ * x/out rotation of `BenchPool` + `measure_block`
+ * (cudalab/evaluator/bench.py:197-309) in native code, with W rotated too.
+ * Synchronizes the stream.
+ */
+int cq_pool_timing(int op, const char* variant, const void* const* w,
+                   const void* const* scale, const void* const* x,
+                   void* const* y, int64_t n_sets, int64_t n, int64_t k,
+                   void* stream, int64_t warmup, int64_t n_launches,
+                   float* kernel_us, double* total_us);
+
+/*
+ * Variant names of `op`, sorted, '\n'-separated, NUL-terminated, written to
+ * buf (capacity cap).  which = CQ_LIST_NORMAL (dispatchable),
+ * CQ_LIST_ALL (also quarantined), CQ_LIST_QUARANTINED, or CQ_LIST_ALIASES
+ * ("alias=target" lines: the reference's variant names accepted as
+ * aliases).  Returns the length needed including the NUL (> 0), or a
+ * negative CQ_* status; if cap is too small nothing is written past cap.
+ * Replaces `int4gemv_variant_list` / `_all_variant_list` /
+ * `_quarantined_variant_list` (kernels/int4gemv/bindings.cpp:258-285) and
+ * the qgemv equivalents (kernels/qgemv/bindings.cpp:251-278).
+ */
+int cq_variants(int op, int which, char* buf, size_t cap);
+
+/*
+ * Host predicate of the vector contract: 1 if the vectorized kernels of
+ * `op` may run on (w, x, k), else 0.  Replaces `int4gemv_vec_contract_ok`
+ * (kernels/int4gemv/int4gemv_common.h:115-121) and `qgemv_vec_contract_ok`
+ * (kernels/qgemv/qgemv_common.h:90-95).
+ */
+int cq_vec_contract_ok(int op, const void* w, const void* x, int64_t k);
+
+/*
+ * Describes, without launching anything, the kernel and launch shape that
+ * cq_int4gemv / cq_qgemv would use for (variant, n, k, w, x): a one-line
+ * "key=value ..." string.  No counterpart in the reference (its variants
+ * have fixed shapes); exposed for tests and tuning records.  Returns the
+ * needed length including the NUL, or a negative CQ_* status.
+ */
+int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
+                       const void* w, const void* x, char* buf, size_t cap);
+
+/*
+ * Message of the last failed call on this thread ("" if none).  Replaces
+ * the TORCH_CHECK error text that the reference's pybind layer raised.
+ */
+const char* cq_last_error(void);
+
+/* Library version string. */
+const char* cq_version(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* CDNAQGEMV_H */

@@ -1,0 +1,179 @@
+"""GPU parity tests of the INT4 W4A16 GEMV (through the C ABI), checked
+against the CPU oracle: the fixed accumulation bound (TOL_K = 2) for every
+variant, shape and input mode; bit-exact properties at full size; the
+reference's negative suite; bit-identity of the scalar fallback."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MODES = ("normal", "zeros", "tiny", "large", "mixed_sign")
+EDGE = [(1, 128), (1, 4096), (3, 128), (16, 256), (8, 128)]
+BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
+         (4096, 11008)]
+EXTRA = [(5, 16384), (7, 16512), (1, 2048), (65, 384), (300, 1280)]
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def _inputs(N, K, mode, seed=0):
+    from cudalab_amd.operators.int4gemv import make_w4, make_x4
+    wp, s, _ = make_w4(N, K, seed=seed, mode=mode)
+    x = make_x4(K, seed=seed + 1, mode=mode)
+    return wp, s, x
+
+
+def test_registry(ext4):
+    v = ext4.variants()
+    assert v == sorted(v)
+    assert "int4gemv_baseline" in v and "int4gemv_cdna4" in v
+    assert ext4.all_variants() == v and ext4.quarantined_variants() == []
+    assert ext4.aliases()["int4gemv_rowtile4_hx"] == "int4gemv_cdna4"
+
+
+@pytest.mark.parametrize("N,K", EDGE + BENCH + EXTRA)
+def test_bound_all_variants_all_modes(ext4, N, K):
+    """Every variant on every mode passes the bound against the oracle's
+    exact values; the product suite's own torch bound agrees."""
+    from cudalab_amd.int4gemv_correctness import arith_ratio
+    for mode in MODES:
+        wp, s, x = _inputs(N, K, mode)
+        wpn, sn, xn = _np(wp), _np(s), _np(x)
+        ex, S = orc.exact_w4(wpn, sn, xn)
+        for v in ext4.variants():
+            announce(f"int4 bound {v} N={N} K={K} mode={mode}")
+            y = ext4.forward(v, wp, s, x)
+            torch.cuda.synchronize()
+            yn = _np(y)
+            r = orc.arith_ratio(yn, ex, S, K)
+            assert np.all(np.isfinite(yn)), (v, mode)
+            assert r.max() <= 1.0, (v, N, K, mode, float(r.max()))
+            r_suite, _, _ = arith_ratio(y, wp, s, x, "float16")
+            assert r_suite <= 1.0, (v, mode, r_suite)
+
+
+def test_zeros_mode_exact_zero(ext4):
+    wp, s, x = _inputs(64, 4096, "zeros")
+    for v in ext4.variants():
+        y = ext4.forward(v, wp, s, x)
+        assert torch.all(y == 0), v
+
+
+@pytest.mark.parametrize("N,K", BENCH)
+def test_full_size_bit_exact_properties(ext4, N, K):
+    """Determinism, odd symmetry y(-x) = -y(x), y(2x) = 2y(x), and row
+    permutation equivariance, all bit-exact."""
+    wp, s, x = _inputs(N, K, "normal", seed=5)
+    perm = torch.randperm(N, generator=torch.Generator().manual_seed(1)).cuda()
+    for v in ("int4gemv_cdna4", "int4gemv_wave_r1", "int4gemv_baseline"):
+        announce(f"int4 properties {v} N={N} K={K}")
+        y = ext4.forward(v, wp, s, x)
+        assert torch.equal(y, ext4.forward(v, wp, s, x)), v
+        assert torch.equal(ext4.forward(v, wp, s, -x), -y), v
+        assert torch.equal(ext4.forward(v, wp, s, x * 2), y * 2), v
+        yp = ext4.forward(v, wp[perm].contiguous(), s[perm].contiguous(), x)
+        assert torch.equal(yp, y[perm]), v
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (11008, 4096), (33, 1024)])
+def test_misaligned_fallback_bit_identical(ext4, N, K):
+    """W_packed and x both 2 bytes past a 16-byte boundary (and each alone):
+    the vector variants take the scalar kernel, bit-identical to the
+    baseline, and within the bound."""
+    wp, s, x = _inputs(N, K, "normal", seed=9)
+    bw = torch.zeros(wp.numel() + 64, dtype=torch.uint8, device="cuda")
+    bx = torch.zeros(K + 32, dtype=torch.float16, device="cuda")
+    wp2 = bw[2:2 + wp.numel()].view(N, K // 2)
+    wp2.copy_(wp)
+    x2 = bx[1:1 + K]
+    x2.copy_(x)
+    assert not ext4.contract_ok(wp2, x) and not ext4.contract_ok(wp, x2)
+    for (Wa, xa) in ((wp2, x2), (wp2, x), (wp, x2)):
+        base = ext4.forward("int4gemv_baseline", Wa, s, xa)
+        for v in ext4.variants():
+            announce(f"int4 fallback {v} N={N} K={K}")
+            assert torch.equal(ext4.forward(v, Wa, s, xa), base), v
+        ex, S = orc.exact_w4(_np(wp), _np(s), _np(x))
+        assert orc.arith_ratio(_np(base), ex, S, K).max() <= 1.0
+
+
+def test_aliases_resolve_to_incumbent(ext4):
+    wp, s, x = _inputs(256, 4096, "normal", seed=3)
+    y = ext4.forward("int4gemv_cdna4", wp, s, x)
+    for a in ext4.aliases():
+        assert torch.equal(ext4.forward(a, wp, s, x), y), a
+
+
+def test_forward_into_and_side_stream(ext4):
+    wp, s, x = _inputs(512, 4096, "mixed_sign", seed=4)
+    y = ext4.forward("int4gemv_cdna4", wp, s, x)
+    out = torch.full((512,), float("nan"), dtype=torch.float16, device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ext4.forward_into("int4gemv_cdna4", wp, s, x, out)
+    st.synchronize()
+    assert torch.equal(out, y)
+
+
+def test_golden_fixtures(ext4):
+    """Committed vectors (tests/golden/) through every variant."""
+    from pathlib import Path
+    d = np.load(Path(__file__).parent / "golden" / "int4gemv_golden.npz")
+    n_cases = int(d["n_cases"])
+    for i in range(n_cases):
+        wp = torch.from_numpy(d[f"wp_{i}"]).cuda()
+        s = torch.from_numpy(d[f"scale_{i}"].view(np.float16)).cuda()
+        x = torch.from_numpy(d[f"x_{i}"].view(np.float16)).cuda()
+        K = x.numel()
+        for v in ext4.variants():
+            y = _np(ext4.forward(v, wp, s, x))
+            r = orc.arith_ratio(y, d[f"exact_{i}"], d[f"S_{i}"], K)
+            assert r.max() <= 1.0, (i, v)
+
+
+@pytest.mark.parametrize("variant", ["int4gemv_baseline", "int4gemv_cdna4",
+                                     "int4gemv_wave_r1", "int4gemv_wave_r2",
+                                     "int4gemv_wave_r4"])
+def test_negative_suite(ext4, variant, tmp_path):
+    from cudalab_amd.int4gemv_negative import run_negative_suite
+    announce(f"int4 negative suite {variant}")
+    doc = run_negative_suite(ext4, out_path=tmp_path / "neg.json",
+                             variant=variant)
+    bad = [c for c in doc["cases"] if not c.get("pass")]
+    assert doc["summary"]["all_pass"], bad
+    assert doc["summary"]["n_total"] == 31
+
+
+def test_product_suite_incumbent(ext4, tmp_path):
+    """The drop-in layer-(a) suite (50 cases) on the incumbent."""
+    from cudalab_amd.operators import get
+    announce("int4 product correctness suite")
+    r = get("int4gemv").run_correctness(ext4, "int4gemv_cdna4",
+                                        out_dir=tmp_path)
+    assert r["all_pass"], r["summary"]["failed"]
+    assert r["summary"]["n_total"] == 50
+
+
+def test_native_and_pool_timing(ext4):
+    from cudalab_amd.ext import pool_timing
+    wp, s, x = _inputs(4096, 4096, "normal", seed=2)
+    out = torch.empty(4096, dtype=torch.float16, device="cuda")
+    d = ext4.native_timing("int4gemv_cdna4", wp, s, x, out, warmup=10,
+                           n_windows=3, launches_per_window=8)
+    assert d["n_windows"] == 3 and len(d["window_median_us"]) == 3
+    assert 0 < d["min_us"] <= d["median_us"] <= d["max_us"]
+    sets = [(wp, s, x, out)]
+    t = pool_timing("int4gemv", "int4gemv_cdna4", sets, warmup=4,
+                    n_launches=16, per_kernel=True)
+    assert len(t["kernel_us"]) == 16 and all(v > 0 for v in t["kernel_us"])
+    assert t["total_us"] > 0
+    with pytest.raises(RuntimeError, match="warmup"):
+        ext4.native_timing("int4gemv_cdna4", wp, s, x, out, warmup=-1)
