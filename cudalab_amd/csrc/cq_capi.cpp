@@ -46,15 +46,21 @@ struct Variant {
 // (kernels/int4gemv/bindings.cpp:46-56).
 constexpr Variant kVariants[] = {
     {"int4gemv_baseline", CQ_OP_INT4GEMV, cq::kScalar, 0, false},
-    {"int4gemv_cdna4", CQ_OP_INT4GEMV, cq::kWave, 0, false},
+    {"int4gemv_cdna4", CQ_OP_INT4GEMV, cq::kLds, 0, false},
     {"int4gemv_wave_r1", CQ_OP_INT4GEMV, cq::kWave, 1, false},
     {"int4gemv_wave_r2", CQ_OP_INT4GEMV, cq::kWave, 2, false},
     {"int4gemv_wave_r4", CQ_OP_INT4GEMV, cq::kWave, 4, false},
+    {"int4gemv_lds_r1", CQ_OP_INT4GEMV, cq::kLds, 1, false},
+    {"int4gemv_lds_r2", CQ_OP_INT4GEMV, cq::kLds, 2, false},
+    {"int4gemv_lds_r4", CQ_OP_INT4GEMV, cq::kLds, 4, false},
     {"qgemv_baseline", CQ_OP_QGEMV, cq::kScalar, 0, false},
-    {"qgemv_cdna4", CQ_OP_QGEMV, cq::kWave, 0, false},
+    {"qgemv_cdna4", CQ_OP_QGEMV, cq::kLds, 0, false},
     {"qgemv_wave_r1", CQ_OP_QGEMV, cq::kWave, 1, false},
     {"qgemv_wave_r2", CQ_OP_QGEMV, cq::kWave, 2, false},
     {"qgemv_wave_r4", CQ_OP_QGEMV, cq::kWave, 4, false},
+    {"qgemv_lds_r1", CQ_OP_QGEMV, cq::kLds, 1, false},
+    {"qgemv_lds_r2", CQ_OP_QGEMV, cq::kLds, 2, false},
+    {"qgemv_lds_r4", CQ_OP_QGEMV, cq::kLds, 4, false},
 };
 
 // The reference's vectorized variant names, accepted so that callers with
@@ -350,7 +356,7 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
     char line[512];
     std::snprintf(line, sizeof line,
                   "variant=%s kernel=%s cw=%d j=%d r=%d block=%d grid=%lld fallback=%d why=%s",
-                  v->name, p.kind == cq::kScalar ? "scalar" : "wave", p.cw, p.j, p.r,
+                  v->name, p.kind == cq::kScalar ? "scalar" : (p.kind == cq::kLds ? "lds" : "wave"), p.cw, p.j, p.r,
                   p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
                   p.why.empty() ? "-" : p.why.c_str());
     return write_out(line, buf, cap);

@@ -12,7 +12,7 @@ namespace cq {
 // Kernel families.  kScalar is the single scalar source shared by the
 // *_baseline variants and by every fallback, so a fallback is bit-identical
 // to the baseline on the same input.  kWave is the CDNA4 wave64 kernel.
-enum Kind : int { kScalar = 0, kWave = 1 };
+enum Kind : int { kScalar = 0, kWave = 1, kLds = 2 };
 
 // Largest reduction length (elements) the wave kernels take; beyond it the
 // scalar kernel runs.  16384 = 8 register-resident x chunks per lane (INT4)

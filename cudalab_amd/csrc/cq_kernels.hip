@@ -335,81 +335,305 @@ __global__ __launch_bounds__(kBlock) void qgemv_wave_kernel(
     }
 }
 
+// ------------------------------------------------------------- wave+LDS
+//
+// Second CDNA4 design: x is staged once per workgroup in LDS, already
+// re-paired for the weight words, instead of every wave loading and
+// re-pairing its own copy.  Per lane the x pairs of its J chunks then come
+// from 4*J ds_read_b128.  Both nibbles of a byte feed one accumulator: the
+// high nibble is taken in place (bits 4-7) under the fp16 exponent of 64,
+// where the mantissa step is 1/16, so ((w & 0x00F000F0) ^ 0x54805480) is
+// the fp16 pair (72+q1, 72+q5) and a packed add of -72 gives (q1, q5)
+// exactly.  Issue order: the workgroup's x pieces, then per row the weight
+// chunks and their group scales, so that each row's arithmetic waits only
+// for its own loads while later rows are still in flight.
+
+template <int CW, int J, int R>
+__global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
+        const uint4* __restrict__ w,         // [n][nchunks] 16-byte chunks
+        const uint16_t* __restrict__ scale,  // [n][nchunks/4]
+        const uint4* __restrict__ x,         // [4*nchunks] 16-byte pieces
+        uint16_t* __restrict__ y, int n, int nchunks) {
+    // [4][nchunks + 1] re-paired x pieces, q-major; column nchunks is zero
+    // and is what lanes past the row end read.
+    extern __shared__ uint4 xs[];
+    constexpr int SLOTS = 64 / CW;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int col = lane % CW;
+    const int slot = lane / CW;
+    const uint32_t ngroups = static_cast<uint32_t>(nchunks) >> 2;
+    const int npieces = 4 * nchunks;
+    const int ldsw = nchunks + 1;
+    const int64_t wave_id =
+        static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (tid >> 6);
+    const int64_t row0 = wave_id * (SLOTS * R) + slot;
+    // Byte offsets fit in 32 bits (the host checks n * k / 2 < 2^32), so
+    // every load is one SGPR base plus one 32-bit VGPR offset.
+    const char* wb = reinterpret_cast<const char*>(w);
+    const char* sb = reinterpret_cast<const char*>(scale);
+    const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
+
+    // (1) this thread's share of x first (npieces <= J * kBlock)
+    uint4 xv[J];
+#pragma unroll
+    for (int i = 0; i < J; ++i) xv[i] = x[std::min(tid + i * kBlock, npieces - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    // (2) weights and group scales, row by row, all in flight together;
+    //     lanes past the row end re-read the last chunk (x is zero there)
+    uint32_t woff[J], soff[J];
+    int xcol[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = col + CW * j;
+        const int cl = c < nchunks ? c : nchunks - 1;
+        xcol[j] = c < nchunks ? c : nchunks;
+        woff[j] = static_cast<uint32_t>(cl) * 16u;
+        soff[j] = static_cast<uint32_t>(cl >> 2) * 2u;
+    }
+    uint4 wv[R][J];
+    uint16_t sv[R][J];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = static_cast<uint32_t>(std::min<int64_t>(row0 + SLOTS * r, n - 1));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            wv[r][j] = *reinterpret_cast<const uint4*>(wb + (row * wrow_bytes + woff[j]));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            sv[r][j] = *reinterpret_cast<const uint16_t*>(sb + (row * ngroups * 2u + soff[j]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // (3) re-pair x: piece = x0..x7 -> [(x0,x4), (x1,x5), (x2,x6), (x3,x7)]
+#pragma unroll
+    for (int i = 0; i < J; ++i) {
+        // unconditional store on the clamped index (threads past the end
+        // rewrite the last piece with the same value), so that no load is
+        // sunk behind a branch
+        const int p = std::min(tid + i * kBlock, npieces - 1);
+        const uint4 v = xv[i];
+        uint4 o;
+        o.x = (v.x & 0xFFFFu) | (v.z << 16);
+        o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+        o.z = (v.y & 0xFFFFu) | (v.w << 16);
+        o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+        xs[(p & 3) * ldsw + (p >> 2)] = o;
+    }
+    if (tid < 4) xs[tid * ldsw + nchunks] = uint4{0, 0, 0, 0};
+    __syncthreads();
+    uint4 xp[J][4];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xp[j][q] = xs[q * ldsw + xcol[j]];
+
+    const f16x2 bias_lo = {static_cast<_Float16>(-1032.0f),
+                           static_cast<_Float16>(-1032.0f)};
+    const f16x2 bias_hi = {static_cast<_Float16>(-72.0f),
+                           static_cast<_Float16>(-72.0f)};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z,
+                                       wv[r][j].w};
+            float d = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t u = words[q];
+                const uint32_t u8 = u >> 8;
+                const f16x2 qa = as_f16x2((u & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
+                const f16x2 qb = as_f16x2((u & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
+                const f16x2 qc = as_f16x2((u8 & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
+                const f16x2 qd = as_f16x2((u8 & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
+                d = __builtin_amdgcn_fdot2(qa, as_f16x2(xp[j][q].x), d, false);
+                d = __builtin_amdgcn_fdot2(qb, as_f16x2(xp[j][q].y), d, false);
+                d = __builtin_amdgcn_fdot2(qc, as_f16x2(xp[j][q].z), d, false);
+                d = __builtin_amdgcn_fdot2(qd, as_f16x2(xp[j][q].w), d, false);
+            }
+            acc = __builtin_fmaf(h2f(sv[r][j]), d, acc);
+        }
+        acc = segment_sum<CW>(acc);
+        const int64_t row = row0 + SLOTS * r;
+        if (col == CW - 1 && row < n) y[row] = f2h(acc);
+    }
+}
+
+template <int CW, int J, int R>
+__global__ __launch_bounds__(kBlock) void qgemv_lds_kernel(
+        const uint4* __restrict__ w,       // [n][nchunks] 16 int8 per chunk
+        const float* __restrict__ scale,   // [n]
+        const uint4* __restrict__ x,       // [2*nchunks] 16-byte pieces
+        uint16_t* __restrict__ y, int n, int nchunks) {
+    // [2][nchunks + 1] re-paired x pieces, q-major; column nchunks is zero
+    extern __shared__ uint4 xs[];
+    constexpr int SLOTS = 64 / CW;
+    constexpr int XPER = (J + 1) / 2;      // x pieces per thread
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int col = lane % CW;
+    const int slot = lane / CW;
+    const int npieces = 2 * nchunks;
+    const int ldsw = nchunks + 1;
+    const int64_t wave_id =
+        static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (tid >> 6);
+    const int64_t row0 = wave_id * (SLOTS * R) + slot;
+    const char* wb = reinterpret_cast<const char*>(w);
+    const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
+
+    uint4 xv[XPER];
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * kBlock, npieces - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t woff[J];
+    int xcol[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = col + CW * j;
+        xcol[j] = c < nchunks ? c : nchunks;
+        woff[j] = static_cast<uint32_t>(c < nchunks ? c : nchunks - 1) * 16u;
+    }
+    uint4 wv[R][J];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = static_cast<uint32_t>(std::min<int64_t>(row0 + SLOTS * r, n - 1));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            wv[r][j] = *reinterpret_cast<const uint4*>(wb + (row * wrow_bytes + woff[j]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // re-pair x: piece = x0..x7 -> [(x0,x2), (x1,x3), (x4,x6), (x5,x7)]
+#pragma unroll
+    for (int i = 0; i < XPER; ++i) {
+        const int p = std::min(tid + i * kBlock, npieces - 1);
+        const uint4 v = xv[i];
+        uint4 o;
+        o.x = (v.x & 0xFFFFu) | (v.y << 16);
+        o.y = (v.x >> 16) | (v.y & 0xFFFF0000u);
+        o.z = (v.z & 0xFFFFu) | (v.w << 16);
+        o.w = (v.z >> 16) | (v.w & 0xFFFF0000u);
+        xs[(p & 1) * ldsw + (p >> 1)] = o;
+    }
+    if (tid < 2) xs[tid * ldsw + nchunks] = uint4{0, 0, 0, 0};
+    __syncthreads();
+    uint4 xp[J][2];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) xp[j][q] = xs[q * ldsw + xcol[j]];
+
+    const f16x2 bias = {static_cast<_Float16>(-1152.0f),
+                        static_cast<_Float16>(-1152.0f)};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z,
+                                       wv[r][j].w};
+            const uint32_t xpair[8] = {xp[j][0].x, xp[j][0].y, xp[j][0].z,
+                                       xp[j][0].w, xp[j][1].x, xp[j][1].y,
+                                       xp[j][1].z, xp[j][1].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t u = words[q];
+                const f16x2 qp = as_f16x2((u & 0x00FF00FFu) ^ 0x64806480u) + bias;
+                const f16x2 qq = as_f16x2(((u >> 8) & 0x00FF00FFu) ^ 0x64806480u) + bias;
+                acc = __builtin_amdgcn_fdot2(qp, as_f16x2(xpair[2 * q]), acc, false);
+                acc = __builtin_amdgcn_fdot2(qq, as_f16x2(xpair[2 * q + 1]), acc, false);
+            }
+        }
+        acc = segment_sum<CW>(acc);
+        const int64_t row = row0 + SLOTS * r;
+        if (col == CW - 1 && row < n) y[row] = f2h(scale[row] * acc);
+    }
+}
+
 // --------------------------------------------------------- instance tables
 
-using Int4WaveFn = void (*)(const uint4*, const uint16_t*, const uint4*,
-                            uint16_t*, int, int);
-using Q8WaveFn = void (*)(const uint4*, const float*, const uint4*,
-                          uint16_t*, int, int);
+using Int4Fn = void (*)(const uint4*, const uint16_t*, const uint4*,
+                        uint16_t*, int, int);
+using Q8Fn = void (*)(const uint4*, const float*, const uint4*, uint16_t*,
+                      int, int);
 
-template <int CW, int J, int R>
-constexpr Int4WaveFn int4_instance() {
-    if constexpr (R <= int4_rmax(J)) return &int4gemv_wave_kernel<CW, J, R>;
-    else return nullptr;
-}
-template <int CW, int J, int R>
-constexpr Q8WaveFn q8_instance() {
-    if constexpr (R <= q8_rmax(J)) return &qgemv_wave_kernel<CW, J, R>;
-    else return nullptr;
-}
+// One traits type per kernel family: the instance for (CW, J, R), or null
+// where the register budget does not allow R rows per lane at J chunks.
+struct Int4Wave {
+    using Fn = Int4Fn;
+    static constexpr int kMaxJ = kInt4MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= int4_rmax(J)) return &int4gemv_wave_kernel<CW, J, R>;
+        else return nullptr;
+    }
+};
+struct Int4Lds {
+    using Fn = Int4Fn;
+    static constexpr int kMaxJ = kInt4MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_kernel<CW, J, R>;
+        else return nullptr;
+    }
+};
+struct Q8Wave {
+    using Fn = Q8Fn;
+    static constexpr int kMaxJ = kQ8MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= q8_rmax(J)) return &qgemv_wave_kernel<CW, J, R>;
+        else return nullptr;
+    }
+};
+struct Q8Lds {
+    using Fn = Q8Fn;
+    static constexpr int kMaxJ = kQ8MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= q8_rmax(J)) return &qgemv_lds_kernel<CW, J, R>;
+        else return nullptr;
+    }
+};
 
 constexpr int r_index(int r) { return r == 1 ? 0 : (r == 2 ? 1 : 2); }
 
-template <int CW, int J>
-Int4WaveFn int4_pick_r(int r) {
-    static constexpr Int4WaveFn t[3] = {int4_instance<CW, J, 1>(),
-                                        int4_instance<CW, J, 2>(),
-                                        int4_instance<CW, J, 4>()};
-    return t[r_index(r)];
-}
-template <int CW, int J>
-Q8WaveFn q8_pick_r(int r) {
-    static constexpr Q8WaveFn t[3] = {q8_instance<CW, J, 1>(),
-                                      q8_instance<CW, J, 2>(),
-                                      q8_instance<CW, J, 4>()};
+template <class F, int CW, int J>
+typename F::Fn pick_r(int r) {
+    static constexpr typename F::Fn t[3] = {F::template get<CW, J, 1>(),
+                                            F::template get<CW, J, 2>(),
+                                            F::template get<CW, J, 4>()};
     return t[r_index(r)];
 }
 
-template <int... Js>
-Int4WaveFn int4_pick_j64(int j, int r, std::integer_sequence<int, Js...>) {
-    Int4WaveFn f = nullptr;
-    ((j == Js + 1 ? (f = int4_pick_r<64, Js + 1>(r), 0) : 0), ...);
-    return f;
-}
-template <int... Js>
-Q8WaveFn q8_pick_j64(int j, int r, std::integer_sequence<int, Js...>) {
-    Q8WaveFn f = nullptr;
-    ((j == Js + 1 ? (f = q8_pick_r<64, Js + 1>(r), 0) : 0), ...);
+template <class F, int... Js>
+typename F::Fn pick_j64(int j, int r, std::integer_sequence<int, Js...>) {
+    typename F::Fn f = nullptr;
+    ((j == Js + 1 ? (f = pick_r<F, 64, Js + 1>(r), 0) : 0), ...);
     return f;
 }
 
-Int4WaveFn int4_wave_fn(int cw, int j, int r) {
-    if (cw == 16 && j == 1) return int4_pick_r<16, 1>(r);
-    if (cw == 32 && j == 1) return int4_pick_r<32, 1>(r);
-    if (cw == 64 && j >= 1 && j <= kInt4MaxJ)
-        return int4_pick_j64(j, r, std::make_integer_sequence<int, kInt4MaxJ>{});
-    return nullptr;
-}
-Q8WaveFn q8_wave_fn(int cw, int j, int r) {
-    if (cw == 16 && j == 1) return q8_pick_r<16, 1>(r);
-    if (cw == 32 && j == 1) return q8_pick_r<32, 1>(r);
-    if (cw == 64 && j >= 1 && j <= kQ8MaxJ)
-        return q8_pick_j64(j, r, std::make_integer_sequence<int, kQ8MaxJ>{});
+template <class F>
+typename F::Fn instance(int cw, int j, int r) {
+    if (cw == 16 && j == 1) return pick_r<F, 16, 1>(r);
+    if (cw == 32 && j == 1) return pick_r<F, 32, 1>(r);
+    if (cw == 64 && j >= 1 && j <= F::kMaxJ)
+        return pick_j64<F>(j, r, std::make_integer_sequence<int, F::kMaxJ>{});
     return nullptr;
 }
 
 // Launch with the argument types taken from the kernel's own signature.
 template <typename... Params>
 hipError_t launch(void (*kernel)(Params...), int64_t grid, int block,
-                  hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1,
-                  std::type_identity_t<Params>... args) {
+                  uint32_t shmem, hipStream_t stream, hipEvent_t ev0,
+                  hipEvent_t ev1, std::type_identity_t<Params>... args) {
     void* argv[] = {static_cast<void*>(&args)...};
     const dim3 g(static_cast<uint32_t>(grid)), b(static_cast<uint32_t>(block));
     if (ev0 == nullptr && ev1 == nullptr)
         return hipLaunchKernel(reinterpret_cast<const void*>(kernel), g, b,
-                               argv, 0, stream);
+                               argv, shmem, stream);
     return hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), g, b,
-                              argv, 0, stream, ev0, ev1, 0);
+                              argv, shmem, stream, ev0, ev1, 0);
 }
 
 int pow2_at_least(int64_t v, int lo) {
@@ -418,23 +642,23 @@ int pow2_at_least(int64_t v, int lo) {
     return p;
 }
 
-// Default rows per lane: the largest R the instance allows that still gives
-// at least `min_waves` waves (8 per CU on a 256-CU part), so the chip is
-// filled and every SIMD holds more than one wave.
-int default_rows(int64_t n, int slots, int rmax) {
+// Default rows per lane (measured on MI355X, streaming and hot): INT4 takes
+// two rows per lane when that still leaves at least 2048 waves (8 per CU),
+// otherwise one; INT8 does best with one row per lane at every bench shape.
+int default_rows_int4(int64_t n, int slots, int rmax) {
     constexpr int64_t min_waves = 2048;
-    for (int r = rmax; r > 1; r >>= 1) {
-        const int64_t waves = (n + slots * r - 1) / (slots * r);
-        if (waves >= min_waves) return r;
-    }
-    return 1;
+    const int r = std::min(2, rmax);
+    const int64_t waves = (n + slots * r - 1) / (slots * r);
+    return (r == 2 && waves >= min_waves) ? 2 : 1;
 }
 
 void finish_wave_plan(Plan& p, int64_t n) {
     const int slots = 64 / p.cw;
     const int64_t rows_per_wave = static_cast<int64_t>(slots) * p.r;
     const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
-    const int64_t block_waves = std::min<int64_t>(kBlock / 64, waves);
+    // the LDS kernels stage x with every thread of a full block
+    const int64_t block_waves =
+        p.kind == kLds ? kBlock / 64 : std::min<int64_t>(kBlock / 64, waves);
     p.block = static_cast<int>(block_waves * 64);
     p.grid = (waves + block_waves - 1) / block_waves;
 }
@@ -470,12 +694,14 @@ Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%32)");
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     const int64_t nchunks = k / 32;
+    if (kind == kLds && n * (k / 2) >= (int64_t{1} << 32))
+        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
     Plan p;
-    p.kind = kWave;
+    p.kind = kind;
     p.cw = pow2_at_least(nchunks, 16);
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
     const int rmax = int4_rmax(p.j);
-    p.r = rows > 0 ? std::min(rows, rmax) : default_rows(n, 64 / p.cw, rmax);
+    p.r = rows > 0 ? std::min(rows, rmax) : default_rows_int4(n, 64 / p.cw, rmax);
     if (p.r == 3) p.r = 2;
     finish_wave_plan(p, n);
     return p;
@@ -488,12 +714,14 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%16)");
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     const int64_t nchunks = k / 16;
+    if (kind == kLds && n * k >= (int64_t{1} << 32))
+        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
     Plan p;
-    p.kind = kWave;
+    p.kind = kind;
     p.cw = pow2_at_least(nchunks, 16);
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
     const int rmax = q8_rmax(p.j);
-    p.r = rows > 0 ? std::min(rows, rmax) : default_rows(n, 64 / p.cw, rmax);
+    p.r = rows > 0 ? std::min(rows, rmax) : 1;
     if (p.r == 3) p.r = 2;
     finish_wave_plan(p, n);
     return p;
@@ -503,14 +731,16 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
                        const void* x, void* y, int64_t n, int64_t k,
                        hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
     if (p.kind == kScalar)
-        return launch(int4gemv_scalar_kernel, p.grid, p.block, stream, ev0, ev1,
-                      static_cast<const uint8_t*>(w),
+        return launch(int4gemv_scalar_kernel, p.grid, p.block, 0, stream, ev0,
+                      ev1, static_cast<const uint8_t*>(w),
                       static_cast<const uint16_t*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    const Int4WaveFn fn = int4_wave_fn(p.cw, p.j, p.r);
+    const Int4Fn fn = p.kind == kLds ? instance<Int4Lds>(p.cw, p.j, p.r)
+                                     : instance<Int4Wave>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    return launch(fn, p.grid, p.block, stream, ev0, ev1,
+    const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 64) : 0;
+    return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
                   static_cast<const uint4*>(w),
                   static_cast<const uint16_t*>(scale),
                   static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
@@ -521,16 +751,17 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                      const void* x, void* y, int64_t n, int64_t k,
                      hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
     if (p.kind == kScalar)
-        return launch(qgemv_scalar_kernel, p.grid, p.block, stream, ev0, ev1,
-                      static_cast<const int8_t*>(w),
+        return launch(qgemv_scalar_kernel, p.grid, p.block, 0, stream, ev0,
+                      ev1, static_cast<const int8_t*>(w),
                       static_cast<const float*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    const Q8WaveFn fn = q8_wave_fn(p.cw, p.j, p.r);
+    const Q8Fn fn = p.kind == kLds ? instance<Q8Lds>(p.cw, p.j, p.r)
+                                   : instance<Q8Wave>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    return launch(fn, p.grid, p.block, stream, ev0, ev1,
-                  static_cast<const uint4*>(w),
-                  static_cast<const float*>(scale),
+    const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 32) : 0;
+    return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
+                  static_cast<const uint4*>(w), static_cast<const float*>(scale),
                   static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
                   static_cast<int>(n), static_cast<int>(k / 16));
 }
