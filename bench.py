@@ -19,6 +19,9 @@ torch.cuda.synchronize() on both sides.
                 per-dispatch average for the same command is committed under
                 profiles/.  `traffic` is the measured HBM bytes per launch
                 from the committed rocprofv3 counter summary, when present.
+                `measured_ceiling` is a plain read of the same bytes per
+                launch (cq_read_ceiling) over an equally cold pool, timed
+                the same way: what one launch of this size can reach.
   cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
                 on the same shape, median of 20 calls, timed on this host
 
@@ -157,7 +160,8 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is "
-              "not supported (the sharded design is described in DESIGN.md)",
+              "not supported (each GPU would run the same kernel on its own "
+              "row shard of W; only the one-GPU figure is measured)",
               file=sys.stderr)
         return 2
     import torch
@@ -181,6 +185,9 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
 
     r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup)
+
+    from cudalab_amd.ext import read_ceiling
+    ceil = read_ceiling(nbytes)
 
     total_s = r["total_us"] * 1e-6
     value = nbytes * args.steps / total_s / 1e9
@@ -232,7 +239,13 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "measured_ceiling": round(ceil["GBps"], 1),
+                     "frac_of_measured_ceiling": round(achieved / ceil["GBps"], 4),
+                     "ceiling_note": "plain streaming read of the same bytes "
+                                     "per launch over an HBM-cold pool "
+                                     "(cq_read_ceiling), same timed-window "
+                                     "caliber"},
         "cpu_baseline": cpu,
         "detail": detail,
     }

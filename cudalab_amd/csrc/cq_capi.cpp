@@ -317,6 +317,40 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
     return CQ_OK;
 }
 
+int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
+                    void* sink, void* stream, int64_t warmup,
+                    int64_t n_launches, double* total_us) {
+    g_last_error.clear();
+    if (bufs == nullptr || sink == nullptr || total_us == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null argument");
+    if (n_bufs < 1 || warmup < 0 || n_launches < 1)
+        return fail(CQ_ERR_INVALID_ARG, "n_bufs, n_launches must be >= 1, warmup >= 0");
+    if (bytes < 16 || bytes % 16 != 0)
+        return fail(CQ_ERR_INVALID_ARG, "bytes must be a positive multiple of 16");
+    for (int64_t i = 0; i < n_bufs; ++i)
+        if (bufs[i] == nullptr || (reinterpret_cast<uintptr_t>(bufs[i]) & 15u) != 0)
+            return fail(CQ_ERR_INVALID_ARG, "buffers must be non-null and 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    for (int64_t i = 0; i < warmup; ++i)
+        if ((e = cq::launch_stream_read(bufs[i % n_bufs], bytes, sink, s)) != hipSuccess)
+            return hip_fail(e, "warmup launch");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    Events win;
+    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    for (int64_t i = 0; i < n_launches; ++i)
+        if ((e = cq::launch_stream_read(bufs[(warmup + i) % n_bufs], bytes, sink, s)) != hipSuccess)
+            return hip_fail(e, "timed launch");
+    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
+        return hip_fail(e, "hipEventElapsedTime");
+    *total_us = static_cast<double>(ms) * 1e3;
+    return CQ_OK;
+}
+
 int cq_variants(int op, int which, char* buf, size_t cap) {
     g_last_error.clear();
     if (op != CQ_OP_INT4GEMV && op != CQ_OP_QGEMV)

@@ -51,4 +51,9 @@ hipError_t launch_q8(const Plan& plan, const void* w, const void* scale,
                      const void* x, void* y, int64_t n, int64_t k,
                      hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
 
+// Plain streaming read of `bytes` (a multiple of 16) from `buf`: the
+// bandwidth ceiling of one launch reading that many bytes.
+hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
+                              hipStream_t stream);
+
 }  // namespace cq

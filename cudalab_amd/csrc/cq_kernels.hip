@@ -93,6 +93,23 @@ __device__ __forceinline__ float segment_sum(float v) {
     return v;
 }
 
+// Workgroups of a launch are dealt round-robin to the 8 XCDs (workgroup i
+// runs on XCD i % 8), and each XCD has its own L2.  This returns a logical
+// block index under which every XCD owns one contiguous range of logical
+// blocks, so each XCD streams one contiguous range of weight rows and
+// writes one contiguous range of y.  It is a bijection on [0, gridDim.x)
+// for any grid size, so it changes which workgroup computes a row, never
+// how the row is computed (outputs are bit-identical to the identity
+// mapping).  Measured on MI355X at the bench shapes: 1-5% faster for INT4
+// and up to 16% for INT8 than the identity mapping.
+__device__ __forceinline__ uint32_t xcd_contiguous_block() {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t b = blockIdx.x, g = gridDim.x;
+    const uint32_t q = g / kXcds, r = g % kXcds;
+    const uint32_t xcd = b % kXcds, idx = b / kXcds;
+    return xcd * q + (xcd < r ? xcd : r) + idx;
+}
+
 // ---------------------------------------------------------------- scalar
 
 __global__ __launch_bounds__(kBlock) void int4gemv_scalar_kernel(
@@ -346,10 +363,12 @@ __global__ __launch_bounds__(kBlock) void qgemv_wave_kernel(
 // the fp16 pair (72+q1, 72+q5) and a packed add of -72 gives (q1, q5)
 // exactly.  Issue order: the workgroup's x pieces, then per row the weight
 // chunks and their group scales, so that each row's arithmetic waits only
-// for its own loads while later rows are still in flight.
+// for its own loads while later rows are still in flight.  Workgroups take
+// their rows through xcd_contiguous_block(); NT (256 or 512 threads) is
+// chosen by the host plan.
 
-template <int CW, int J, int R>
-__global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
         const uint4* __restrict__ w,         // [n][nchunks] 16-byte chunks
         const uint16_t* __restrict__ scale,  // [n][nchunks/4]
         const uint4* __restrict__ x,         // [4*nchunks] 16-byte pieces
@@ -365,8 +384,9 @@ __global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
     const uint32_t ngroups = static_cast<uint32_t>(nchunks) >> 2;
     const int npieces = 4 * nchunks;
     const int ldsw = nchunks + 1;
+    const uint32_t blk = xcd_contiguous_block();
     const int64_t wave_id =
-        static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (tid >> 6);
+        static_cast<int64_t>(blk) * (blockDim.x >> 6) + (tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
     // Byte offsets fit in 32 bits (the host checks n * k / 2 < 2^32), so
     // every load is one SGPR base plus one 32-bit VGPR offset.
@@ -374,10 +394,11 @@ __global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
     const char* sb = reinterpret_cast<const char*>(scale);
     const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
 
-    // (1) this thread's share of x first (npieces <= J * kBlock)
-    uint4 xv[J];
+    // (1) this thread's share of x first (npieces <= 256 * J <= NT * XPER)
+    constexpr int XPER = (256 * J + NT - 1) / NT;
+    uint4 xv[XPER];
 #pragma unroll
-    for (int i = 0; i < J; ++i) xv[i] = x[std::min(tid + i * kBlock, npieces - 1)];
+    for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * NT, npieces - 1)];
     __builtin_amdgcn_sched_barrier(0);
     // (2) weights and group scales, row by row, all in flight together;
     //     lanes past the row end re-read the last chunk (x is zero there)
@@ -406,11 +427,11 @@ __global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
     __builtin_amdgcn_sched_barrier(0);
     // (3) re-pair x: piece = x0..x7 -> [(x0,x4), (x1,x5), (x2,x6), (x3,x7)]
 #pragma unroll
-    for (int i = 0; i < J; ++i) {
+    for (int i = 0; i < XPER; ++i) {
         // unconditional store on the clamped index (threads past the end
         // rewrite the last piece with the same value), so that no load is
         // sunk behind a branch
-        const int p = std::min(tid + i * kBlock, npieces - 1);
+        const int p = std::min(tid + i * NT, npieces - 1);
         const uint4 v = xv[i];
         uint4 o;
         o.x = (v.x & 0xFFFFu) | (v.z << 16);
@@ -460,8 +481,8 @@ __global__ __launch_bounds__(kBlock) void int4gemv_lds_kernel(
     }
 }
 
-template <int CW, int J, int R>
-__global__ __launch_bounds__(kBlock) void qgemv_lds_kernel(
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void qgemv_lds_kernel(
         const uint4* __restrict__ w,       // [n][nchunks] 16 int8 per chunk
         const float* __restrict__ scale,   // [n]
         const uint4* __restrict__ x,       // [2*nchunks] 16-byte pieces
@@ -469,22 +490,23 @@ __global__ __launch_bounds__(kBlock) void qgemv_lds_kernel(
     // [2][nchunks + 1] re-paired x pieces, q-major; column nchunks is zero
     extern __shared__ uint4 xs[];
     constexpr int SLOTS = 64 / CW;
-    constexpr int XPER = (J + 1) / 2;      // x pieces per thread
+    constexpr int XPER = (128 * J + NT - 1) / NT;   // x pieces per thread
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int col = lane % CW;
     const int slot = lane / CW;
     const int npieces = 2 * nchunks;
     const int ldsw = nchunks + 1;
+    const uint32_t blk = xcd_contiguous_block();
     const int64_t wave_id =
-        static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (tid >> 6);
+        static_cast<int64_t>(blk) * (blockDim.x >> 6) + (tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
     const char* wb = reinterpret_cast<const char*>(w);
     const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
 
     uint4 xv[XPER];
 #pragma unroll
-    for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * kBlock, npieces - 1)];
+    for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * NT, npieces - 1)];
     __builtin_amdgcn_sched_barrier(0);
     uint32_t woff[J];
     int xcol[J];
@@ -506,7 +528,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_lds_kernel(
     // re-pair x: piece = x0..x7 -> [(x0,x2), (x1,x3), (x4,x6), (x5,x7)]
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
-        const int p = std::min(tid + i * kBlock, npieces - 1);
+        const int p = std::min(tid + i * NT, npieces - 1);
         const uint4 v = xv[i];
         uint4 o;
         o.x = (v.x & 0xFFFFu) | (v.y << 16);
@@ -550,6 +572,31 @@ __global__ __launch_bounds__(kBlock) void qgemv_lds_kernel(
     }
 }
 
+// ------------------------------------------------- read-only ceiling
+//
+// A plain streaming read of `bytes` (16-byte loads, 4 per thread).  The
+// loaded words are folded and compared with `key`, a launch argument the
+// compiler cannot see, so the loads cannot be removed; the store to `sink`
+// runs only if a thread's fold equals the key (harmless either way: sink is
+// the caller's scratch word).  It is the measured bandwidth ceiling of one
+// launch that reads the same number of bytes as a GEMV call.
+__global__ __launch_bounds__(kBlock) void stream_read_kernel(
+        const uint4* __restrict__ p, uint32_t* __restrict__ sink, int64_t n16,
+        uint32_t key) {
+    constexpr int PER = 4;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlock * PER + threadIdx.x;
+    uint4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int64_t idx = base + static_cast<int64_t>(i) * kBlock;
+        v[i] = p[idx < n16 ? idx : n16 - 1];
+    }
+    uint32_t a = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (a == key) sink[0] = a;
+}
+
 // --------------------------------------------------------- instance tables
 
 using Int4Fn = void (*)(const uint4*, const uint16_t*, const uint4*,
@@ -568,12 +615,13 @@ struct Int4Wave {
         else return nullptr;
     }
 };
+template <int NT>
 struct Int4Lds {
     using Fn = Int4Fn;
     static constexpr int kMaxJ = kInt4MaxJ;
     template <int CW, int J, int R>
     static constexpr Fn get() {
-        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_kernel<CW, J, R>;
+        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_kernel<CW, J, R, NT>;
         else return nullptr;
     }
 };
@@ -586,12 +634,13 @@ struct Q8Wave {
         else return nullptr;
     }
 };
+template <int NT>
 struct Q8Lds {
     using Fn = Q8Fn;
     static constexpr int kMaxJ = kQ8MaxJ;
     template <int CW, int J, int R>
     static constexpr Fn get() {
-        if constexpr (R <= q8_rmax(J)) return &qgemv_lds_kernel<CW, J, R>;
+        if constexpr (R <= q8_rmax(J)) return &qgemv_lds_kernel<CW, J, R, NT>;
         else return nullptr;
     }
 };
@@ -652,13 +701,24 @@ int default_rows_int4(int64_t n, int slots, int rmax) {
     return (r == 2 && waves >= min_waves) ? 2 : 1;
 }
 
-void finish_wave_plan(Plan& p, int64_t n) {
+// Workgroup size of the LDS kernels.  512 threads halve the number of
+// workgroups that stage x; measured on MI355X this pays for INT4 with two
+// rows per lane as long as the grid still has a workgroup for every CU
+// (256), and nowhere else at the bench shapes.
+constexpr int64_t kCus = 256;
+int lds_threads(bool int4, int r, int64_t waves) {
+    if (int4 && r == 2 && (waves + 7) / 8 >= kCus) return 512;
+    return kBlock;
+}
+
+void finish_wave_plan(Plan& p, int64_t n, bool int4) {
     const int slots = 64 / p.cw;
     const int64_t rows_per_wave = static_cast<int64_t>(slots) * p.r;
     const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
     // the LDS kernels stage x with every thread of a full block
     const int64_t block_waves =
-        p.kind == kLds ? kBlock / 64 : std::min<int64_t>(kBlock / 64, waves);
+        p.kind == kLds ? lds_threads(int4, p.r, waves) / 64
+                       : std::min<int64_t>(kBlock / 64, waves);
     p.block = static_cast<int>(block_waves * 64);
     p.grid = (waves + block_waves - 1) / block_waves;
 }
@@ -703,7 +763,7 @@ Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
     const int rmax = int4_rmax(p.j);
     p.r = rows > 0 ? std::min(rows, rmax) : default_rows_int4(n, 64 / p.cw, rmax);
     if (p.r == 3) p.r = 2;
-    finish_wave_plan(p, n);
+    finish_wave_plan(p, n, true);
     return p;
 }
 
@@ -723,7 +783,7 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
     const int rmax = q8_rmax(p.j);
     p.r = rows > 0 ? std::min(rows, rmax) : 1;
     if (p.r == 3) p.r = 2;
-    finish_wave_plan(p, n);
+    finish_wave_plan(p, n, false);
     return p;
 }
 
@@ -736,8 +796,10 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
                       static_cast<const uint16_t*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    const Int4Fn fn = p.kind == kLds ? instance<Int4Lds>(p.cw, p.j, p.r)
-                                     : instance<Int4Wave>(p.cw, p.j, p.r);
+    const Int4Fn fn =
+        p.kind == kWave ? instance<Int4Wave>(p.cw, p.j, p.r)
+        : p.block == 512 ? instance<Int4Lds<512>>(p.cw, p.j, p.r)
+                         : instance<Int4Lds<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 64) : 0;
     return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
@@ -756,14 +818,24 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                       static_cast<const float*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    const Q8Fn fn = p.kind == kLds ? instance<Q8Lds>(p.cw, p.j, p.r)
-                                   : instance<Q8Wave>(p.cw, p.j, p.r);
+    // INT8 plans always use kBlock threads for the LDS kernels
+    const Q8Fn fn = p.kind == kWave ? instance<Q8Wave>(p.cw, p.j, p.r)
+                                    : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 32) : 0;
     return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
                   static_cast<const uint4*>(w), static_cast<const float*>(scale),
                   static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
                   static_cast<int>(n), static_cast<int>(k / 16));
+}
+
+hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
+                              hipStream_t stream) {
+    const int64_t n16 = bytes / 16;
+    const int64_t grid = (n16 + kBlock * 4 - 1) / (kBlock * 4);
+    return launch(stream_read_kernel, grid, kBlock, 0, stream, nullptr,
+                  nullptr, static_cast<const uint4*>(buf),
+                  static_cast<uint32_t*>(sink), n16, 0x9E3779B9u);
 }
 
 }  // namespace cq

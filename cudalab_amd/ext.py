@@ -389,3 +389,29 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
         _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")
     return {"total_us": tot.value,
             "kernel_us": [float(v) for v in ku] if ku is not None else None}
+
+
+def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
+                 pool_bytes: int = 512 << 20, device: str = "cuda") -> dict:
+    """Bandwidth ceiling of one launch reading `nbytes`: a plain streaming
+    read kernel (cq_read_ceiling) over a rotating pool of distinct buffers
+    totalling more than `pool_bytes` (HBM-cold), timed like pool_timing."""
+    lib = _capi.load()
+    nbytes = (int(nbytes) + 15) // 16 * 16
+    n = max(2, pool_bytes // nbytes + 1)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(n)]
+    for b in bufs:
+        b.fill_(0x5A)
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    arr = (ctypes.c_void_p * n)(*[b.data_ptr() for b in bufs])
+    tot = ctypes.c_double(0.0)
+    dev = bufs[0].device
+    with torch.cuda.device(dev):
+        s = torch.cuda.current_stream(dev)
+        st = lib.cq_read_ceiling(arr, n, nbytes, sink.data_ptr(), s.cuda_stream,
+                                 warmup, n_launches, ctypes.byref(tot))
+    if st != _capi.CQ_OK:
+        _fail(f"read_ceiling failed (status {st}): {_capi.last_error()}")
+    us = tot.value / n_launches
+    return {"bytes": nbytes, "us_per_call": us, "GBps": nbytes / us / 1e3,
+            "pool_buffers": n}

@@ -115,12 +115,15 @@ int cq_native_timing(int op, const char* variant, const void* w,
 /*
  * Rotating-pool timing for HBM-cold ("streaming") measurement: launch i
  * (0 <= i < warmup + n_launches) uses set (i % n_sets) of the caller's
- * arrays w[], scale[], x[], y[].  For each of the n_launches timed launches
- * kernel_us[i] (caller-owned, may be NULL) receives the kernel's own device
- * duration from start/stop events attached to the dispatch
- * (hipExtLaunchKernel), and *total_us the event time of the whole timed
- * window.  No counterpart in the reference's C++ layer: it restates the
- * x/out rotation of `BenchPool` + `measure_block`
+ * arrays w[], scale[], x[], y[].  *total_us receives the event time of
+ * the timed window (two events around n_launches back-to-back launches).
+ * If kernel_us (caller-owned, length n_launches) is non-NULL, every timed
+ * launch also carries start/stop events on the dispatch itself
+ * (hipExtLaunchKernel) and kernel_us[i] receives their difference; on
+ * MI355X these per-dispatch events read about 4 us even for an empty
+ * kernel, so they are only meaningful for long kernels.  No counterpart in
+ * the reference's C++ layer: it restates the x/out rotation of
+ * `BenchPool` + `measure_block`
  * (cudalab/evaluator/bench.py:197-309) in native code, with W rotated too.
  * Synchronizes the stream.
  */
@@ -129,6 +132,20 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
                    void* const* y, int64_t n_sets, int64_t n, int64_t k,
                    void* stream, int64_t warmup, int64_t n_launches,
                    float* kernel_us, double* total_us);
+
+/*
+ * Read-only ceiling: `n_launches` back-to-back launches of a plain
+ * streaming-read kernel, launch i reading `bytes` (a multiple of 16) from
+ * bufs[i % n_bufs] (16-byte aligned device buffers), after `warmup`
+ * untimed launches; *total_us receives the event time of the timed window.
+ * `sink` is a device buffer of at least 4 bytes that the kernel may write.
+ * No counterpart in the reference: it measures the bandwidth one launch
+ * can reach for a given byte count on this device (the ceiling a GEMV call
+ * of the same bytes is compared against).  Synchronizes the stream.
+ */
+int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
+                    void* sink, void* stream, int64_t warmup,
+                    int64_t n_launches, double* total_us);
 
 /*
  * Variant names of `op`, sorted, '\n'-separated, NUL-terminated, written to

@@ -26,7 +26,7 @@ def _declared_functions() -> set[str]:
 
 def test_header_declares_the_abi():
     names = _declared_functions()
-    assert {"cq_int4gemv", "cq_qgemv", "cq_native_timing", "cq_pool_timing",
+    assert {"cq_int4gemv", "cq_qgemv", "cq_native_timing", "cq_pool_timing", "cq_read_ceiling",
             "cq_variants", "cq_vec_contract_ok", "cq_describe_launch",
             "cq_last_error", "cq_version"} <= names
 
@@ -74,20 +74,22 @@ def test_vector_contract_predicate():
     assert not ok("qgemv", 0x1008, 0x2000, 64)
 
 
-@pytest.mark.parametrize("n,k,kernel,cw,j,r", [
-    (4096, 4096, "lds", 64, 2, 2),
-    (11008, 4096, "lds", 64, 2, 2),
-    (4096, 11008, "lds", 64, 6, 1),
-    (1024, 4096, "lds", 64, 2, 1),
-    (4096, 1024, "lds", 32, 1, 1),
-    (1, 128, "lds", 16, 1, 1),
-    (5, 16384, "lds", 64, 8, 1),
+@pytest.mark.parametrize("n,k,kernel,cw,j,r,block", [
+    (4096, 4096, "lds", 64, 2, 2, 512),
+    (11008, 4096, "lds", 64, 2, 2, 512),
+    (4096, 11008, "lds", 64, 6, 1, 256),
+    (1024, 4096, "lds", 64, 2, 1, 256),
+    (4096, 1024, "lds", 32, 1, 1, 256),
+    (1, 128, "lds", 16, 1, 1, 256),
+    (5, 16384, "lds", 64, 8, 1, 256),
+    # two rows per lane but fewer than 256 workgroups at 512 threads
+    (3000, 4096, "lds", 64, 2, 1, 256),
 ])
-def test_int4_launch_plans(n, k, kernel, cw, j, r):
+def test_int4_launch_plans(n, k, kernel, cw, j, r, block):
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", n, k, 4096, 8192)
     assert (d["kernel"], int(d["cw"]), int(d["j"]), int(d["r"])) == (kernel, cw, j, r)
-    assert d["fallback"] == "0" and int(d["block"]) == 256
-    rows_per_block = (64 // cw) * r * 4
+    assert d["fallback"] == "0" and int(d["block"]) == block
+    rows_per_block = (64 // cw) * r * (block // 64)
     assert int(d["grid"]) == -(-n // rows_per_block)
 
 
@@ -136,3 +138,14 @@ def test_argument_errors_without_launch():
     st = lib.cq_pool_timing(0, b"int4gemv_cdna4", None, None, None, None, 1,
                             4, 128, None, 0, 1, None, None)
     assert st == _capi.CQ_ERR_INVALID_ARG
+    tot = ctypes.c_double()
+    bufs = (ctypes.c_void_p * 2)(0x1000, 0x2008)
+    st = lib.cq_read_ceiling(bufs, 2, 4096, P, None, 0, 1, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG and "aligned" in _capi.last_error()
+    bufs = (ctypes.c_void_p * 1)(0x1000)
+    st = lib.cq_read_ceiling(bufs, 1, 4100, P, None, 0, 1, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG and "multiple of 16" in _capi.last_error()
+    st = lib.cq_read_ceiling(bufs, 1, 4096, P, None, 0, 0, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG
+    st = lib.cq_read_ceiling(bufs, 1, 4096, None, None, 0, 1, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()

@@ -17,7 +17,10 @@ MODES = ("normal", "zeros", "tiny", "large", "mixed_sign")
 EDGE = [(1, 128), (1, 4096), (3, 128), (16, 256), (8, 128)]
 BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
-EXTRA = [(5, 16384), (7, 16512), (1, 2048), (65, 384), (300, 1280)]
+# (4099, 4096): two rows per lane on 512-thread workgroups with a partial
+# last workgroup and a grid (257) that is not a multiple of the 8 XCDs
+EXTRA = [(5, 16384), (7, 16512), (1, 2048), (65, 384), (300, 1280),
+         (4099, 4096)]
 
 
 def _np(t: torch.Tensor) -> np.ndarray:

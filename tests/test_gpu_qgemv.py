@@ -15,7 +15,9 @@ MODES = ("normal", "zeros", "tiny", "large", "mixed_sign")
 EDGE = [(1, 1), (1, 4096), (4096, 1), (16, 13), (8, 7)]
 BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
-EXTRA = [(5, 16384), (3, 16400), (17, 16), (9, 48), (300, 1040), (2, 8192)]
+# (1001, 4096): a grid (251 workgroups) that is not a multiple of the 8 XCDs
+EXTRA = [(5, 16384), (3, 16400), (17, 16), (9, 48), (300, 1040), (2, 8192),
+         (1001, 4096)]
 
 
 def _np(t):
