@@ -1,10 +1,12 @@
 """Short text summaries of rocprofv3 output directories.
 
-Two reports, both printed to stdout:
+Three reports, all printed to stdout:
 
   trace    per-kernel dispatch durations from a `--kernel-trace --stats` run
            (count, mean, median, min, max, and the median gap between
            consecutive dispatches of the same kernel)
+  counters per-dispatch medians of every counter in one or more `--pmc`
+           runs, for the kernels matching each --match string
   traffic  HBM bytes per dispatch of one kernel from two `--pmc` runs
            (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same
            counter reads for a calibration copy of known size in the same
@@ -16,6 +18,8 @@ Reads rocprofv3's CSV output (`-f csv`: *_kernel_trace.csv,
 
 Usage:
   python -m cudalab_amd.evaluator.rocprof_summary trace DIR [--match S]
+  python -m cudalab_amd.evaluator.rocprof_summary counters DIR [DIR ...]
+      --match S [--match S ...]
   python -m cudalab_amd.evaluator.rocprof_summary traffic --fetch DIR
       --write DIR --match S --calib-match S --calib-bytes B
       [--shape N K] [--json-out FILE]
@@ -72,6 +76,21 @@ def dispatch_times(d: Path) -> dict[str, list[tuple[int, int]]]:
     for v in by.values():
         v.sort()
     return by
+
+
+def counter_names(d: Path) -> list[str]:
+    names: set[str] = set()
+    tables = _csv_rows(d, "counter_collection.csv")
+    for header, rows in tables:
+        ci = _col(header, "Counter_Name")
+        names.update(r[ci] for r in rows)
+    if not tables:
+        for db in _dbs(d):
+            con = sqlite3.connect(db)
+            names.update(r[0] for r in con.execute(
+                "select distinct counter_name from counters_collection"))
+            con.close()
+    return sorted(names)
 
 
 def counter_values(d: Path, counter: str) -> dict[str, list[float]]:
@@ -186,6 +205,23 @@ def report_traffic(fetch: Path, write: Path, match: str, calib_match: str,
     return "\n".join(lines), out
 
 
+def report_counters(dirs: list[Path], matches: list[str]) -> str:
+    lines = []
+    for match in matches:
+        lines.append(f"kernel matching {match!r}:")
+        for d in dirs:
+            for counter in counter_names(d):
+                by = counter_values(d, counter)
+                hits = [k for k in by if match in k]
+                if not hits:
+                    continue
+                kname = max(hits, key=lambda k: len(by[k]))
+                v = by[kname]
+                lines.append(f"  {counter:<28} median {statistics.median(v):>14.2f}"
+                             f"   ({len(v)} dispatches; {d.name})")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -193,6 +229,9 @@ def main(argv=None) -> int:
     t.add_argument("dir", type=Path)
     t.add_argument("--match", default=None)
     t.add_argument("--top", type=int, default=8)
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", type=Path, nargs="+")
+    c.add_argument("--match", action="append", required=True)
     f = sub.add_parser("traffic")
     f.add_argument("--fetch", type=Path, required=True)
     f.add_argument("--write", type=Path, required=True)
@@ -205,6 +244,9 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         print(report_trace(a.dir, a.match, a.top))
+        return 0
+    if a.cmd == "counters":
+        print(report_counters(a.dirs, a.match))
         return 0
     text, rec = report_traffic(a.fetch, a.write, a.match, a.calib_match,
                                a.calib_bytes)
