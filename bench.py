@@ -105,15 +105,8 @@ def graph_loop(ext, variant: str, sets, per_graph: int = 256,
 
 
 def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
-    from cudalab_amd.evaluator.bench import cold_pool_sets
-    if op == "int4gemv":
-        from cudalab_amd.operators.int4gemv import device_random_set, int4_bytes
-        nbytes = int4_bytes(N, K)
-    else:
-        from cudalab_amd.operators.qgemv import device_random_set, q8_bytes
-        nbytes = q8_bytes(N, K)
-    n = cold_pool_sets(nbytes) if mode == "streaming" else 1
-    return [device_random_set(N, K, seed + 100000 + i) for i in range(n)], nbytes
+    from cudalab_amd.evaluator.sweep import make_sets as _make_sets
+    return _make_sets(op, N, K, mode, seed)
 
 
 def cpu_baseline(N: int, K: int, sets) -> dict:

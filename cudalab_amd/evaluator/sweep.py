@@ -1,0 +1,119 @@
+"""Shape sweep of the GEMV path on one GPU: µs per call, effective GB/s,
+fraction of HBM peak and of the measured read ceiling, for INT4 and INT8
+over the reference's five bench shapes (cudalab/operators/int4gemv.py:30-36
+lists the same matrix) in streaming (HBM-cold pool) and hot (one resident
+set) modes.
+
+Timing caliber: K back-to-back launches on one stream between two HIP
+events (cq_pool_timing), the same as bench.py's headline.  The read
+ceiling is cq_read_ceiling over an equally cold pool of the same bytes.
+
+Usage: python -m cudalab_amd.evaluator.sweep [--steps K] [--json FILE]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import torch
+
+from ..ext import pool_timing, read_ceiling
+from ..build import build
+from .bench import cold_pool_sets
+
+HBM_PEAK_GBS = 8000.0
+SHAPES = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
+          (4096, 11008)]
+OPS = {"int4gemv": "int4gemv_cdna4", "qgemv": "qgemv_cdna4"}
+
+
+def algorithmic_bytes(op: str, N: int, K: int) -> int:
+    if op == "int4gemv":
+        from ..operators.int4gemv import int4_bytes
+        return int4_bytes(N, K)
+    from ..operators.qgemv import q8_bytes
+    return q8_bytes(N, K)
+
+
+def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
+    """Input sets drawn on the device: a pool of more than 512 MiB of
+    distinct sets for "streaming", one set for "hot"."""
+    if op == "int4gemv":
+        from ..operators.int4gemv import device_random_set
+    else:
+        from ..operators.qgemv import device_random_set
+    nbytes = algorithmic_bytes(op, N, K)
+    n = cold_pool_sets(nbytes) if mode == "streaming" else 1
+    return [device_random_set(N, K, seed + 100000 + i) for i in range(n)], nbytes
+
+
+def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
+    torch.cuda.synchronize()
+    r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
+                    per_kernel=False)
+    torch.cuda.synchronize()
+    return r["total_us"] / steps
+
+
+def run(ops=tuple(OPS), shapes=SHAPES, modes=("streaming", "hot"),
+        steps: int = 2000, warmup: int = 200) -> list[dict]:
+    out = []
+    for op in ops:
+        ext = build(op)
+        variant = OPS[op]
+        for (N, K) in shapes:
+            for mode in modes:
+                sets, nbytes = make_sets(op, N, K, mode)
+                plan = ext.describe(variant, sets[0][0], sets[0][2])
+                us = window_us(op, variant, sets, steps, warmup)
+                rec = {"op": op, "variant": variant, "N": N, "K": K,
+                       "mode": mode, "pool_sets": len(sets),
+                       "bytes_per_call": nbytes, "us_per_call": round(us, 4),
+                       "GBps": round(nbytes / us / 1e3, 1),
+                       "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                       "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r",
+                                                      "block", "grid")}}
+                if mode == "streaming":
+                    c = read_ceiling(nbytes, warmup=warmup, n_launches=steps)
+                    rec["ceiling_us"] = round(c["us_per_call"], 4)
+                    rec["frac_ceiling"] = round(c["us_per_call"] / us, 4)
+                out.append(rec)
+                del sets
+                torch.cuda.empty_cache()
+    return out
+
+
+def table(records: list[dict]) -> str:
+    lines = [f"{'op':<9} {'N':>6} {'K':>6} {'mode':<9} {'us/call':>8} "
+             f"{'GB/s':>7} {'%peak':>6} {'ceil_us':>8} {'%ceil':>6}  plan"]
+    for r in records:
+        p = r["plan"]
+        plan = f"{p['kernel']} cw={p['cw']} j={p['j']} r={p['r']} block={p['block']} grid={p['grid']}"
+        ceil = (f"{r['ceiling_us']:>8.3f} {100 * r['frac_ceiling']:>5.1f}%"
+                if "ceiling_us" in r else f"{'-':>8} {'-':>6}")
+        lines.append(f"{r['op']:<9} {r['N']:>6} {r['K']:>6} {r['mode']:<9} "
+                     f"{r['us_per_call']:>8.3f} {r['GBps']:>7.0f} "
+                     f"{100 * r['frac_peak']:>5.1f}% {ceil}  {plan}")
+    return "\n".join(lines)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--json", default=None)
+    a = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("sweep: no GPU visible", file=sys.stderr)
+        return 1
+    recs = run(steps=a.steps, warmup=a.warmup)
+    print(table(recs), flush=True)
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(recs, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
