@@ -46,6 +46,16 @@ class CqTiming(ctypes.Structure):
     ]
 
 
+class CqProblem(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("x", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+    ]
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _cstr = ctypes.c_char_p
@@ -54,6 +64,10 @@ _cstr = ctypes.c_char_p
 SIGNATURES = {
     "cq_int4gemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "cq_qgemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "cq_int4gemv_grouped": (ctypes.c_int, [_cstr, ctypes.POINTER(CqProblem),
+                                           _i64, _i64, _vp]),
+    "cq_qgemv_grouped": (ctypes.c_int, [_cstr, ctypes.POINTER(CqProblem),
+                                        _i64, _i64, _vp]),
     "cq_native_timing": (ctypes.c_int, [
         ctypes.c_int, _cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
         _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(CqTiming)]),

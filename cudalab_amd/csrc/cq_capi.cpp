@@ -155,6 +155,49 @@ int run_one(int op, const char* variant, const void* w, const void* scale,
     return CQ_OK;
 }
 
+int run_grouped(int op, const char* variant, const cq_gemv_problem_t* probs,
+                int64_t count, int64_t k, void* stream) {
+    g_last_error.clear();
+    if (probs == nullptr) return fail(CQ_ERR_INVALID_ARG, "problems is NULL");
+    if (count < 1 || count > INT_MAX)
+        return fail(CQ_ERR_INVALID_ARG, "n_problems must be >= 1, got " + std::to_string(count));
+    const Variant* v = nullptr;
+    for (int64_t i = 0; i < count; ++i) {
+        const cq_gemv_problem_t& q = probs[i];
+        const int st = check_call(op, variant, &v, q.w, q.scale, q.x, q.y, q.n, k);
+        if (st != CQ_OK) {
+            g_last_error = "problem " + std::to_string(i) + ": " + g_last_error;
+            return st;
+        }
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto one = [&](const cq_gemv_problem_t& q) {
+        const cq::Plan p = make_plan(op, *v, q.n, k, q.w, q.x);
+        return launch_plan(op, p, q.w, q.scale, q.x, q.y, q.n, k, s, nullptr, nullptr);
+    };
+    for (int64_t off = 0; off < count; off += cq::kMaxGroup) {
+        const int c = static_cast<int>(std::min<int64_t>(cq::kMaxGroup, count - off));
+        hipError_t e = hipSuccess;
+        cq::Plan p;
+        cq::GroupProblem gp[cq::kMaxGroup];
+        for (int i = 0; i < c; ++i) {
+            const cq_gemv_problem_t& q = probs[off + i];
+            gp[i] = {q.w, q.scale, q.x, q.y, q.n};
+        }
+        if (v->kind == cq::kLds)
+            p = op == CQ_OP_INT4GEMV ? cq::plan_int4_group(v->rows, gp, c, k)
+                                     : cq::plan_q8_group(v->rows, gp, c, k);
+        if (v->kind == cq::kLds && p.kind == cq::kLds) {
+            e = op == CQ_OP_INT4GEMV ? cq::launch_int4_group(p, gp, c, k, s)
+                                     : cq::launch_q8_group(p, gp, c, k, s);
+        } else {
+            for (int i = 0; i < c && e == hipSuccess; ++i) e = one(probs[off + i]);
+        }
+        if (e != hipSuccess) return hip_fail(e, "grouped launch");
+    }
+    return CQ_OK;
+}
+
 std::string join_sorted(std::vector<std::string> names) {
     std::sort(names.begin(), names.end());
     std::string s;
@@ -201,6 +244,16 @@ int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
 int cq_qgemv(const char* variant, const void* w_q, const void* scale,
              const void* x, void* y, int64_t n, int64_t k, void* stream) {
     return run_one(CQ_OP_QGEMV, variant, w_q, scale, x, y, n, k, stream);
+}
+
+int cq_int4gemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
+                        int64_t n_problems, int64_t k, void* stream) {
+    return run_grouped(CQ_OP_INT4GEMV, variant, problems, n_problems, k, stream);
+}
+
+int cq_qgemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
+                     int64_t n_problems, int64_t k, void* stream) {
+    return run_grouped(CQ_OP_QGEMV, variant, problems, n_problems, k, stream);
 }
 
 int cq_native_timing(int op, const char* variant, const void* w,

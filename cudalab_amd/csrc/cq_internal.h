@@ -51,6 +51,29 @@ hipError_t launch_q8(const Plan& plan, const void* w, const void* scale,
                      const void* x, void* y, int64_t n, int64_t k,
                      hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
 
+// Grouped launches: up to kMaxGroup independent problems of one k in one
+// launch of the LDS kernels.
+constexpr int kMaxGroup = 8;
+
+struct GroupProblem {
+    const void* w;
+    const void* scale;
+    const void* x;
+    void* y;
+    int64_t n;
+};
+
+// Plan of a grouped launch of `count` (1..kMaxGroup) problems.  Kind kLds
+// when every problem meets the vector contract and the LDS kernels' size
+// limits; otherwise kind kScalar with `fallback` set, meaning "launch the
+// problems one by one" (each then gets its own plan).  `rows` as above.
+Plan plan_int4_group(int rows, const GroupProblem* probs, int count, int64_t k);
+Plan plan_q8_group(int rows, const GroupProblem* probs, int count, int64_t k);
+hipError_t launch_int4_group(const Plan& plan, const GroupProblem* probs,
+                             int count, int64_t k, hipStream_t stream);
+hipError_t launch_q8_group(const Plan& plan, const GroupProblem* probs,
+                           int count, int64_t k, hipStream_t stream);
+
 // Plain streaming read of `bytes` (a multiple of 16) from `buf`: the
 // bandwidth ceiling of one launch reading that many bytes.
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

@@ -49,6 +49,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 namespace cq {
@@ -367,15 +368,16 @@ __global__ __launch_bounds__(kBlock) void qgemv_wave_kernel(
 // their rows through xcd_contiguous_block(); NT (256 or 512 threads) is
 // chosen by the host plan.
 
+// The rows of logical workgroup `blk` of one INT4 problem.  `xs` is the
+// workgroup's LDS: [4][nchunks + 1] re-paired x pieces, q-major; column
+// nchunks is zero and is what lanes past the row end read.
 template <int CW, int J, int R, int NT>
-__global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
+__device__ __forceinline__ void int4_lds_rows(
         const uint4* __restrict__ w,         // [n][nchunks] 16-byte chunks
         const uint16_t* __restrict__ scale,  // [n][nchunks/4]
         const uint4* __restrict__ x,         // [4*nchunks] 16-byte pieces
-        uint16_t* __restrict__ y, int n, int nchunks) {
-    // [4][nchunks + 1] re-paired x pieces, q-major; column nchunks is zero
-    // and is what lanes past the row end read.
-    extern __shared__ uint4 xs[];
+        uint16_t* __restrict__ y, int n, int nchunks, uint32_t blk,
+        uint4* __restrict__ xs) {
     constexpr int SLOTS = 64 / CW;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -384,9 +386,8 @@ __global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
     const uint32_t ngroups = static_cast<uint32_t>(nchunks) >> 2;
     const int npieces = 4 * nchunks;
     const int ldsw = nchunks + 1;
-    const uint32_t blk = xcd_contiguous_block();
     const int64_t wave_id =
-        static_cast<int64_t>(blk) * (blockDim.x >> 6) + (tid >> 6);
+        static_cast<int64_t>(blk) * (NT >> 6) + (tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
     // Byte offsets fit in 32 bits (the host checks n * k / 2 < 2^32), so
     // every load is one SGPR base plus one 32-bit VGPR offset.
@@ -481,14 +482,15 @@ __global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
     }
 }
 
+// The rows of logical workgroup `blk` of one INT8 problem; `xs` holds
+// [2][nchunks + 1] re-paired x pieces, q-major, column nchunks zero.
 template <int CW, int J, int R, int NT>
-__global__ __launch_bounds__(NT) void qgemv_lds_kernel(
+__device__ __forceinline__ void q8_lds_rows(
         const uint4* __restrict__ w,       // [n][nchunks] 16 int8 per chunk
         const float* __restrict__ scale,   // [n]
         const uint4* __restrict__ x,       // [2*nchunks] 16-byte pieces
-        uint16_t* __restrict__ y, int n, int nchunks) {
-    // [2][nchunks + 1] re-paired x pieces, q-major; column nchunks is zero
-    extern __shared__ uint4 xs[];
+        uint16_t* __restrict__ y, int n, int nchunks, uint32_t blk,
+        uint4* __restrict__ xs) {
     constexpr int SLOTS = 64 / CW;
     constexpr int XPER = (128 * J + NT - 1) / NT;   // x pieces per thread
     const int tid = threadIdx.x;
@@ -497,9 +499,8 @@ __global__ __launch_bounds__(NT) void qgemv_lds_kernel(
     const int slot = lane / CW;
     const int npieces = 2 * nchunks;
     const int ldsw = nchunks + 1;
-    const uint32_t blk = xcd_contiguous_block();
     const int64_t wave_id =
-        static_cast<int64_t>(blk) * (blockDim.x >> 6) + (tid >> 6);
+        static_cast<int64_t>(blk) * (NT >> 6) + (tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
     const char* wb = reinterpret_cast<const char*>(w);
     const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
@@ -572,6 +573,76 @@ __global__ __launch_bounds__(NT) void qgemv_lds_kernel(
     }
 }
 
+// One problem per launch.
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
+        const uint4* __restrict__ w, const uint16_t* __restrict__ scale,
+        const uint4* __restrict__ x, uint16_t* __restrict__ y, int n,
+        int nchunks) {
+    extern __shared__ uint4 xs[];
+    int4_lds_rows<CW, J, R, NT>(w, scale, x, y, n, nchunks,
+                                xcd_contiguous_block(), xs);
+}
+
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void qgemv_lds_kernel(
+        const uint4* __restrict__ w, const float* __restrict__ scale,
+        const uint4* __restrict__ x, uint16_t* __restrict__ y, int n,
+        int nchunks) {
+    extern __shared__ uint4 xs[];
+    q8_lds_rows<CW, J, R, NT>(w, scale, x, y, n, nchunks,
+                              xcd_contiguous_block(), xs);
+}
+
+// Several independent problems of one k per launch (grouped GEMV).  The
+// problem table travels by value in the kernel arguments; logical
+// workgroups [start[p], start[p+1]) belong to problem p, and each computes
+// exactly the rows it would compute in a launch of that problem alone, so
+// the outputs are bit-identical to separate launches.
+struct GroupArgs {
+    const void* w[kMaxGroup];
+    const void* scale[kMaxGroup];
+    const void* x[kMaxGroup];
+    void* y[kMaxGroup];
+    int n[kMaxGroup];
+    uint32_t start[kMaxGroup + 1];
+    int count;
+};
+
+__device__ __forceinline__ int group_of(const GroupArgs& g, uint32_t lb) {
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i) p += (i < g.count && lb >= g.start[i]) ? 1 : 0;
+    return p;
+}
+
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void int4gemv_lds_group_kernel(GroupArgs g,
+                                                                 int nchunks) {
+    extern __shared__ uint4 xs[];
+    const uint32_t lb = xcd_contiguous_block();
+    const int p = group_of(g, lb);
+    int4_lds_rows<CW, J, R, NT>(static_cast<const uint4*>(g.w[p]),
+                                static_cast<const uint16_t*>(g.scale[p]),
+                                static_cast<const uint4*>(g.x[p]),
+                                static_cast<uint16_t*>(g.y[p]), g.n[p], nchunks,
+                                lb - g.start[p], xs);
+}
+
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void qgemv_lds_group_kernel(GroupArgs g,
+                                                             int nchunks) {
+    extern __shared__ uint4 xs[];
+    const uint32_t lb = xcd_contiguous_block();
+    const int p = group_of(g, lb);
+    q8_lds_rows<CW, J, R, NT>(static_cast<const uint4*>(g.w[p]),
+                              static_cast<const float*>(g.scale[p]),
+                              static_cast<const uint4*>(g.x[p]),
+                              static_cast<uint16_t*>(g.y[p]), g.n[p], nchunks,
+                              lb - g.start[p], xs);
+}
+
+
 // ------------------------------------------------- read-only ceiling
 //
 // A plain streaming read of `bytes` (16-byte loads, 4 per thread).  The
@@ -641,6 +712,30 @@ struct Q8Lds {
     template <int CW, int J, int R>
     static constexpr Fn get() {
         if constexpr (R <= q8_rmax(J)) return &qgemv_lds_kernel<CW, J, R, NT>;
+        else return nullptr;
+    }
+};
+
+using Int4GroupFn = void (*)(GroupArgs, int);
+using Q8GroupFn = void (*)(GroupArgs, int);
+
+template <int NT>
+struct Int4LdsGroup {
+    using Fn = Int4GroupFn;
+    static constexpr int kMaxJ = kInt4MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_group_kernel<CW, J, R, NT>;
+        else return nullptr;
+    }
+};
+template <int NT>
+struct Q8LdsGroup {
+    using Fn = Q8GroupFn;
+    static constexpr int kMaxJ = kQ8MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= q8_rmax(J)) return &qgemv_lds_group_kernel<CW, J, R, NT>;
         else return nullptr;
     }
 };
@@ -827,6 +922,122 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                   static_cast<const uint4*>(w), static_cast<const float*>(scale),
                   static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
                   static_cast<int>(n), static_cast<int>(k / 16));
+}
+
+namespace {
+
+// Shared part of the grouped plans: the plan of the whole group's rows for
+// the LDS kernel (cw, j from k; r and block from the total row count), or a
+// "launch one by one" plan when any problem cannot take the LDS kernel.
+template <typename PlanFn, typename OkFn>
+Plan group_plan(PlanFn plan_one, OkFn lds_ok, int rows,
+                const GroupProblem* probs, int count, int64_t k) {
+    Plan p;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!lds_ok(probs[i])) {
+            p.fallback = true;
+            p.why = "a problem misses the vector contract or the LDS limits";
+            return p;
+        }
+        total += probs[i].n;
+    }
+    p = plan_one(kLds, rows, total, k, probs[0].w, probs[0].x);
+    if (p.kind != kLds) {
+        p.kind = kScalar;
+        p.fallback = true;
+    }
+    return p;
+}
+
+// Per-problem workgroup counts of plan `p` and their prefix sums.
+bool fill_group(const Plan& p, const GroupProblem* probs, int count,
+                GroupArgs& g, int64_t& grid) {
+    const int64_t rows_per_wave = static_cast<int64_t>(64 / p.cw) * p.r;
+    const int64_t block_waves = p.block / 64;
+    int64_t start = 0;
+    for (int i = 0; i < kMaxGroup; ++i) {
+        g.w[i] = g.scale[i] = g.x[i] = nullptr;
+        g.y[i] = nullptr;
+        g.n[i] = 0;
+    }
+    for (int i = 0; i < count; ++i) {
+        const int64_t waves = (probs[i].n + rows_per_wave - 1) / rows_per_wave;
+        g.w[i] = probs[i].w;
+        g.scale[i] = probs[i].scale;
+        g.x[i] = probs[i].x;
+        g.y[i] = probs[i].y;
+        g.n[i] = static_cast<int>(probs[i].n);
+        g.start[i] = static_cast<uint32_t>(start);
+        start += (waves + block_waves - 1) / block_waves;
+        if (start > INT32_MAX) return false;
+    }
+    for (int i = count; i <= kMaxGroup; ++i) g.start[i] = static_cast<uint32_t>(start);
+    g.count = count;
+    grid = start;
+    return true;
+}
+
+template <typename Fn>
+hipError_t launch_group(Fn fn, const Plan& p, const GroupArgs& g,
+                        int64_t grid, uint32_t shmem, int nchunks,
+                        hipStream_t stream) {
+    if (fn == nullptr) return hipErrorInvalidConfiguration;
+    GroupArgs a = g;
+    int nc = nchunks;
+    void* argv[] = {static_cast<void*>(&a), static_cast<void*>(&nc)};
+    return hipLaunchKernel(reinterpret_cast<const void*>(fn),
+                           dim3(static_cast<uint32_t>(grid)),
+                           dim3(static_cast<uint32_t>(p.block)), argv, shmem,
+                           stream);
+}
+
+}  // namespace
+
+Plan plan_int4_group(int rows, const GroupProblem* probs, int count, int64_t k) {
+    return group_plan(
+        plan_int4,
+        [k](const GroupProblem& q) {
+            return int4_contract_ok(q.w, q.x, k) && k <= kMaxWaveK &&
+                   q.n * (k / 2) < (int64_t{1} << 32);
+        },
+        rows, probs, count, k);
+}
+
+Plan plan_q8_group(int rows, const GroupProblem* probs, int count, int64_t k) {
+    return group_plan(
+        plan_q8,
+        [k](const GroupProblem& q) {
+            return q8_contract_ok(q.w, q.x, k) && k <= kMaxWaveK &&
+                   q.n * k < (int64_t{1} << 32);
+        },
+        rows, probs, count, k);
+}
+
+hipError_t launch_int4_group(const Plan& p, const GroupProblem* probs,
+                             int count, int64_t k, hipStream_t stream) {
+    if (p.kind != kLds || count < 1 || count > kMaxGroup)
+        return hipErrorInvalidConfiguration;
+    GroupArgs g;
+    int64_t grid = 0;
+    if (!fill_group(p, probs, count, g, grid)) return hipErrorInvalidConfiguration;
+    const Int4GroupFn fn = p.block == 512
+                               ? instance<Int4LdsGroup<512>>(p.cw, p.j, p.r)
+                               : instance<Int4LdsGroup<kBlock>>(p.cw, p.j, p.r);
+    return launch_group(fn, p, g, grid, static_cast<uint32_t>(2 * k + 64),
+                        static_cast<int>(k / 32), stream);
+}
+
+hipError_t launch_q8_group(const Plan& p, const GroupProblem* probs,
+                           int count, int64_t k, hipStream_t stream) {
+    if (p.kind != kLds || count < 1 || count > kMaxGroup || p.block != kBlock)
+        return hipErrorInvalidConfiguration;
+    GroupArgs g;
+    int64_t grid = 0;
+    if (!fill_group(p, probs, count, g, grid)) return hipErrorInvalidConfiguration;
+    return launch_group(instance<Q8LdsGroup<kBlock>>(p.cw, p.j, p.r), p, g, grid,
+                        static_cast<uint32_t>(2 * k + 32),
+                        static_cast<int>(k / 16), stream);
 }
 
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

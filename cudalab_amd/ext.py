@@ -51,6 +51,9 @@ class _OpExt:
         self._aliases = _capi.aliases(self.op)
         self._fn = (self._lib.cq_int4gemv if self.op == "int4gemv"
                     else self._lib.cq_qgemv)
+        self._grouped_fn = (self._lib.cq_int4gemv_grouped
+                            if self.op == "int4gemv"
+                            else self._lib.cq_qgemv_grouped)
 
     # ---- registry (bindings.cpp variant lists) ----
     def variants(self) -> list[str]:
@@ -153,6 +156,46 @@ class _OpExt:
         self._validate_inputs(W, scale, x)
         self._validate_out(W, out)
         self._launch(variant, W, scale, x, out)
+
+    def forward_grouped(self, variant: str, problems) -> None:
+        """Several independent GEMVs sharing K, in as few launches as the
+        variant allows (one per 8 problems for the CDNA4 LDS variants).
+        `problems` is a sequence of (W, scale, x, out) tuples, each checked
+        exactly as forward_into checks its arguments; every `out` is then
+        bit-identical to forward_into(variant, W, scale, x, out).  No
+        counterpart in the reference (its modules launch one problem at a
+        time)."""
+        self._lookup(variant)
+        problems = list(problems)
+        if not problems:
+            _fail("problems 不能为空 (problems must be a non-empty list)")
+        K = None
+        dev = None
+        for (W, scale, x, out) in problems:
+            self._validate_inputs(W, scale, x)
+            self._validate_out(W, out)
+            if K is None:
+                K, dev = self._k(W), W.device
+            elif self._k(W) != K:
+                _fail(f"分组调用的所有问题必须有相同的 K: {K} vs {self._k(W)} "
+                      "(all problems of a grouped call must share K)")
+            elif W.device != dev:
+                _fail("分组调用的所有问题必须在同一 CUDA 设备上 "
+                      "(all problems of a grouped call must be on one device)")
+        arr = (_capi.CqProblem * len(problems))()
+        for i, (W, scale, x, out) in enumerate(problems):
+            arr[i].w = W.data_ptr()
+            arr[i].scale = scale.data_ptr()
+            arr[i].x = x.data_ptr()
+            arr[i].y = out.data_ptr()
+            arr[i].n = W.size(0)
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = self._grouped_fn(variant.encode(), arr, len(problems), K,
+                                  stream)
+        if st != _capi.CQ_OK:
+            _fail(f"{self.op} grouped launch failed (status {st}): "
+                  f"{_capi.last_error()}")
 
     def native_timing(self, variant: str, W: torch.Tensor,
                       scale: torch.Tensor, x: torch.Tensor,

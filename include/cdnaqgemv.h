@@ -86,6 +86,32 @@ int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
 int cq_qgemv(const char* variant, const void* w_q, const void* scale,
              const void* x, void* y, int64_t n, int64_t k, void* stream);
 
+/* One problem of a grouped call: device pointers and its row count. */
+typedef struct cq_gemv_problem {
+    const void* w;      /* w_packed (int4gemv) or w_q (qgemv) */
+    const void* scale;
+    const void* x;
+    void* y;
+    int64_t n;
+} cq_gemv_problem_t;
+
+/*
+ * Grouped GEMV: n_problems independent problems of one operator that share
+ * k, enqueued with as few launches as possible (one launch per 8 problems
+ * for the CDNA4 LDS variants; the other variants, and any 8-problem batch
+ * in which a problem misses the vector contract, launch problem by
+ * problem).  Each y is bit-identical to a cq_int4gemv / cq_qgemv call of
+ * the same variant on the same problem.  Every problem is checked as a
+ * single call would be before anything is launched.  No counterpart in the
+ * reference (its variants launch one problem at a time): it serves decode
+ * steps whose projections are independent (q/k/v; gate/up) and pays the
+ * per-launch cost once per batch.
+ */
+int cq_int4gemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
+                        int64_t n_problems, int64_t k, void* stream);
+int cq_qgemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
+                     int64_t n_problems, int64_t k, void* stream);
+
 /* Result of cq_native_timing; all times are per launch, microseconds. */
 typedef struct cq_timing {
     int64_t warmup;

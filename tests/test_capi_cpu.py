@@ -27,6 +27,7 @@ def _declared_functions() -> set[str]:
 def test_header_declares_the_abi():
     names = _declared_functions()
     assert {"cq_int4gemv", "cq_qgemv", "cq_native_timing", "cq_pool_timing", "cq_read_ceiling",
+            "cq_int4gemv_grouped", "cq_qgemv_grouped",
             "cq_variants", "cq_vec_contract_ok", "cq_describe_launch",
             "cq_last_error", "cq_version"} <= names
 
@@ -149,3 +150,27 @@ def test_argument_errors_without_launch():
     assert st == _capi.CQ_ERR_INVALID_ARG
     st = lib.cq_read_ceiling(bufs, 1, 4096, None, None, 0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()
+
+
+def test_grouped_argument_errors_without_launch():
+    lib = _capi.load()
+    P = 0x1000
+    probs = (_capi.CqProblem * 3)()
+    for i in range(3):
+        probs[i].w = probs[i].scale = probs[i].x = probs[i].y = P
+        probs[i].n = 8
+    st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", None, 1, 128, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and "NULL" in _capi.last_error()
+    st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 0, 128, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and "n_problems" in _capi.last_error()
+    st = lib.cq_int4gemv_grouped(b"nope", probs, 3, 128, None)
+    assert st == _capi.CQ_ERR_UNKNOWN_VARIANT
+    st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 3, 100, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and "128" in _capi.last_error()
+    probs[1].y = None
+    st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 3, 128, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and _capi.last_error().startswith("problem 1:")
+    probs[1].y = P
+    probs[2].n = 0
+    st = lib.cq_qgemv_grouped(b"qgemv_cdna4", probs, 3, 16, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and _capi.last_error().startswith("problem 2:")

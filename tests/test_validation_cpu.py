@@ -131,3 +131,17 @@ def test_registry_api(e4, e8):
     assert get("int4gemv").variants(e4) == e4.variants()
     with pytest.raises(KeyError):
         get("rmsnorm")
+
+
+def test_grouped_checks(e4, monkeypatch):
+    """forward_grouped checks every problem as forward_into does, and
+    rejects an empty list and mixed K before anything is launched."""
+    W, s, x = _int4_base()
+    o = torch.zeros(8, dtype=torch.float16)
+    assert "non-empty" in _msg(lambda: e4.forward_grouped("int4gemv_cdna4", []))
+    assert "未知 int4gemv 变体" in _msg(lambda: e4.forward_grouped("zzz", [(W, s, x, o)]))
+    assert "CUDA 张量" in _msg(lambda: e4.forward_grouped("int4gemv_cdna4", [(W, s, x, o)]))
+    for name in ("_validate_w", "_validate_scale", "_validate_x", "_validate_out"):
+        monkeypatch.setattr(type(e4), name, lambda self, *a: None)
+    W2 = torch.zeros(8, 256, dtype=torch.uint8)
+    assert "share K" in _msg(lambda: e4.forward_grouped("int4gemv_cdna4", [(W, s, x, o), (W2, s, x, o)]))
