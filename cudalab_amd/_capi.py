@@ -25,13 +25,22 @@ CQ_ERR_BUFFER_TOO_SMALL = 4
 
 CQ_OP_INT4GEMV = 0
 CQ_OP_QGEMV = 1
+CQ_OP_GEMV_F16 = 2
+CQ_OP_GEMV_F32 = 3
+
+CQ_DTYPE_F16 = 0
+CQ_DTYPE_F32 = 1
 
 CQ_LIST_NORMAL = 0
 CQ_LIST_ALL = 1
 CQ_LIST_QUARANTINED = 2
 CQ_LIST_ALIASES = 3
 
-OPS = {"int4gemv": CQ_OP_INT4GEMV, "qgemv": CQ_OP_QGEMV}
+# operator ids by name; "gemv" lists its (dtype-independent) registry
+# through the fp16 id
+OPS = {"int4gemv": CQ_OP_INT4GEMV, "qgemv": CQ_OP_QGEMV,
+       "gemv": CQ_OP_GEMV_F16, "gemv_f16": CQ_OP_GEMV_F16,
+       "gemv_f32": CQ_OP_GEMV_F32}
 
 
 class CqTiming(ctypes.Structure):
@@ -64,6 +73,8 @@ _cstr = ctypes.c_char_p
 SIGNATURES = {
     "cq_int4gemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "cq_qgemv": (ctypes.c_int, [_cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "cq_gemv": (ctypes.c_int, [_cstr, ctypes.c_int, _vp, _vp, _vp, _i64, _i64,
+                               _vp]),
     "cq_int4gemv_grouped": (ctypes.c_int, [_cstr, ctypes.POINTER(CqProblem),
                                            _i64, _i64, _vp]),
     "cq_qgemv_grouped": (ctypes.c_int, [_cstr, ctypes.POINTER(CqProblem),

@@ -99,7 +99,7 @@ def build_library(verbose: bool = False) -> Path:
 
 
 def build(op: str):
-    """Extension object for `op` ("int4gemv" | "qgemv"), bound to the built
+    """Extension object for `op` ("int4gemv" | "qgemv" | "gemv"), bound to the built
     library.  Mirrors `cudalab/build.py:build(op)` (which returned the JIT
     module); raises if the library has not been built."""
     from . import ext

@@ -61,6 +61,14 @@ constexpr Variant kVariants[] = {
     {"qgemv_lds_r1", CQ_OP_QGEMV, cq::kLds, 1, false},
     {"qgemv_lds_r2", CQ_OP_QGEMV, cq::kLds, 2, false},
     {"qgemv_lds_r4", CQ_OP_QGEMV, cq::kLds, 4, false},
+    // gemv: one registry for both dtypes (listed under CQ_OP_GEMV_F16).
+    // gemv_splitk4 keeps the reference's quarantined name for callers that
+    // name it explicitly (kernels/gemv/bindings.cpp:50-80); it runs the
+    // scalar kernel here: a split-K GEMV needs a cross-workgroup workspace,
+    // which is what the reference quarantined it for.
+    {"gemv_baseline", CQ_OP_GEMV_F16, cq::kScalar, 0, false},
+    {"gemv_cdna4", CQ_OP_GEMV_F16, cq::kLds, 0, false},
+    {"gemv_splitk4", CQ_OP_GEMV_F16, cq::kScalar, 0, true},
 };
 
 // The reference's vectorized variant names, accepted so that callers with
@@ -82,18 +90,33 @@ constexpr Alias kAliases[] = {
     {"qgemv_vec16_scale", "qgemv_cdna4", CQ_OP_QGEMV},
     {"qgemv_warp_vec16", "qgemv_cdna4", CQ_OP_QGEMV},
     {"qgemv_warp_vec16_ilp4", "qgemv_cdna4", CQ_OP_QGEMV},
+    {"gemv_vec4_row", "gemv_cdna4", CQ_OP_GEMV_F16},
+    {"gemv_warp_vec4", "gemv_cdna4", CQ_OP_GEMV_F16},
 };
 
+bool valid_op(int op) {
+    return op == CQ_OP_INT4GEMV || op == CQ_OP_QGEMV || op == CQ_OP_GEMV_F16 ||
+           op == CQ_OP_GEMV_F32;
+}
+
+bool is_gemv(int op) { return op == CQ_OP_GEMV_F16 || op == CQ_OP_GEMV_F32; }
+
+// Registry key of an operator id: both gemv dtypes share one registry.
+int family(int op) { return op == CQ_OP_GEMV_F32 ? CQ_OP_GEMV_F16 : op; }
+
 const char* op_name(int op) {
-    return op == CQ_OP_INT4GEMV ? "int4gemv" : (op == CQ_OP_QGEMV ? "qgemv" : "?");
+    if (op == CQ_OP_INT4GEMV) return "int4gemv";
+    if (op == CQ_OP_QGEMV) return "qgemv";
+    return is_gemv(op) ? "gemv" : "?";
 }
 
 const Variant* find_variant(int op, const char* name) {
     if (name == nullptr) return nullptr;
+    const int f = family(op);
     for (const Alias& a : kAliases)
-        if (a.op == op && std::strcmp(a.alias, name) == 0) name = a.target;
+        if (a.op == f && std::strcmp(a.alias, name) == 0) name = a.target;
     for (const Variant& v : kVariants)
-        if (v.op == op && std::strcmp(v.name, name) == 0) return &v;
+        if (v.op == f && std::strcmp(v.name, name) == 0) return &v;
     return nullptr;
 }
 
@@ -102,14 +125,16 @@ const Variant* find_variant(int op, const char* name) {
 int check_call(int op, const char* variant, const Variant** out,
                const void* w, const void* scale, const void* x,
                const void* y, int64_t n, int64_t k) {
-    if (op != CQ_OP_INT4GEMV && op != CQ_OP_QGEMV)
+    if (!valid_op(op))
         return fail(CQ_ERR_INVALID_ARG, "unknown operator id " + std::to_string(op));
     if (variant == nullptr) return fail(CQ_ERR_INVALID_ARG, "variant name is NULL");
     const Variant* v = find_variant(op, variant);
     if (v == nullptr)
         return fail(CQ_ERR_UNKNOWN_VARIANT,
                     std::string("unknown ") + op_name(op) + " variant '" + variant + "'");
-    if (w == nullptr || scale == nullptr || x == nullptr || y == nullptr)
+    // gemv has no scale (the argument is ignored and may be NULL)
+    if (w == nullptr || (scale == nullptr && !is_gemv(op)) || x == nullptr ||
+        y == nullptr)
         return fail(CQ_ERR_INVALID_ARG, "null device pointer");
     if (n <= 0 || n > INT_MAX)
         return fail(CQ_ERR_INVALID_ARG, "n must be in [1, 2^31-1], got " + std::to_string(n));
@@ -122,19 +147,24 @@ int check_call(int op, const char* variant, const Variant** out,
     return CQ_OK;
 }
 
+int gemv_dtype(int op) { return op == CQ_OP_GEMV_F32 ? cq::kF32 : cq::kF16; }
+
 cq::Plan make_plan(int op, const Variant& v, int64_t n, int64_t k,
                    const void* w, const void* x) {
-    return op == CQ_OP_INT4GEMV ? cq::plan_int4(v.kind, v.rows, n, k, w, x)
-                                : cq::plan_q8(v.kind, v.rows, n, k, w, x);
+    if (op == CQ_OP_INT4GEMV) return cq::plan_int4(v.kind, v.rows, n, k, w, x);
+    if (op == CQ_OP_QGEMV) return cq::plan_q8(v.kind, v.rows, n, k, w, x);
+    return cq::plan_gemv(v.kind, gemv_dtype(op), n, k, w, x);
 }
 
 hipError_t launch_plan(int op, const cq::Plan& p, const void* w,
                        const void* scale, const void* x, void* y, int64_t n,
                        int64_t k, hipStream_t stream, hipEvent_t ev0,
                        hipEvent_t ev1) {
-    return op == CQ_OP_INT4GEMV
-               ? cq::launch_int4(p, w, scale, x, y, n, k, stream, ev0, ev1)
-               : cq::launch_q8(p, w, scale, x, y, n, k, stream, ev0, ev1);
+    if (op == CQ_OP_INT4GEMV)
+        return cq::launch_int4(p, w, scale, x, y, n, k, stream, ev0, ev1);
+    if (op == CQ_OP_QGEMV)
+        return cq::launch_q8(p, w, scale, x, y, n, k, stream, ev0, ev1);
+    return cq::launch_gemv(p, gemv_dtype(op), w, x, y, n, k, stream, ev0, ev1);
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -246,6 +276,16 @@ int cq_qgemv(const char* variant, const void* w_q, const void* scale,
     return run_one(CQ_OP_QGEMV, variant, w_q, scale, x, y, n, k, stream);
 }
 
+int cq_gemv(const char* variant, int dtype, const void* w, const void* x,
+            void* y, int64_t n, int64_t k, void* stream) {
+    if (dtype != CQ_DTYPE_F16 && dtype != CQ_DTYPE_F32) {
+        g_last_error = "unknown gemv dtype " + std::to_string(dtype);
+        return CQ_ERR_INVALID_ARG;
+    }
+    return run_one(dtype == CQ_DTYPE_F32 ? CQ_OP_GEMV_F32 : CQ_OP_GEMV_F16,
+                   variant, w, nullptr, x, y, n, k, stream);
+}
+
 int cq_int4gemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
                         int64_t n_problems, int64_t k, void* stream) {
     return run_grouped(CQ_OP_INT4GEMV, variant, problems, n_problems, k, stream);
@@ -318,7 +358,8 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
                    void* stream, int64_t warmup, int64_t n_launches,
                    float* kernel_us, double* total_us) {
     g_last_error.clear();
-    if (w == nullptr || scale == nullptr || x == nullptr || y == nullptr)
+    if (w == nullptr || (scale == nullptr && !is_gemv(op)) || x == nullptr ||
+        y == nullptr)
         return fail(CQ_ERR_INVALID_ARG, "null set array");
     if (n_sets < 1) return fail(CQ_ERR_INVALID_ARG, "n_sets must be >= 1");
     if (warmup < 0) return fail(CQ_ERR_INVALID_ARG, "warmup must be >= 0");
@@ -326,14 +367,16 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
     std::vector<cq::Plan> plans(static_cast<size_t>(n_sets));
     const Variant* v = nullptr;
     for (int64_t i = 0; i < n_sets; ++i) {
-        const int st = check_call(op, variant, &v, w[i], scale[i], x[i], y[i], n, k);
+        const void* sc = scale != nullptr ? scale[i] : nullptr;
+        const int st = check_call(op, variant, &v, w[i], sc, x[i], y[i], n, k);
         if (st != CQ_OK) return st;
         plans[static_cast<size_t>(i)] = make_plan(op, *v, n, k, w[i], x[i]);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     auto go = [&](int64_t i, hipEvent_t e0, hipEvent_t e1) {
         const size_t si = static_cast<size_t>(i % n_sets);
-        return launch_plan(op, plans[si], w[si], scale[si], x[si], y[si], n, k, s, e0, e1);
+        return launch_plan(op, plans[si], w[si], scale != nullptr ? scale[si] : nullptr,
+                           x[si], y[si], n, k, s, e0, e1);
     };
     hipError_t e;
     for (int64_t i = 0; i < warmup; ++i)
@@ -406,8 +449,9 @@ int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
 
 int cq_variants(int op, int which, char* buf, size_t cap) {
     g_last_error.clear();
-    if (op != CQ_OP_INT4GEMV && op != CQ_OP_QGEMV)
+    if (!valid_op(op))
         return fail(-CQ_ERR_INVALID_ARG, "unknown operator id " + std::to_string(op));
+    op = family(op);
     std::vector<std::string> names;
     if (which == CQ_LIST_ALIASES) {
         for (const Alias& a : kAliases)
@@ -429,6 +473,7 @@ int cq_variants(int op, int which, char* buf, size_t cap) {
 int cq_vec_contract_ok(int op, const void* w, const void* x, int64_t k) {
     if (op == CQ_OP_INT4GEMV) return cq::int4_contract_ok(w, x, k) ? 1 : 0;
     if (op == CQ_OP_QGEMV) return cq::q8_contract_ok(w, x, k) ? 1 : 0;
+    if (is_gemv(op)) return cq::gemv_contract_ok(gemv_dtype(op), w, x, k) ? 1 : 0;
     return 0;
 }
 

@@ -74,6 +74,15 @@ hipError_t launch_int4_group(const Plan& plan, const GroupProblem* probs,
 hipError_t launch_q8_group(const Plan& plan, const GroupProblem* probs,
                            int count, int64_t k, hipStream_t stream);
 
+// FP16/FP32 GEMV (the reference's kernels/gemv): element type of W, x, y.
+enum Dtype : int { kF16 = 0, kF32 = 1 };
+bool gemv_contract_ok(int dtype, const void* w, const void* x, int64_t k);
+Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
+               const void* x);
+hipError_t launch_gemv(const Plan& plan, int dtype, const void* w,
+                       const void* x, void* y, int64_t n, int64_t k,
+                       hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
+
 // Plain streaming read of `bytes` (a multiple of 16) from `buf`: the
 // bandwidth ceiling of one launch reading that many bytes.
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

@@ -643,6 +643,145 @@ __global__ __launch_bounds__(NT) void qgemv_lds_group_kernel(GroupArgs g,
 }
 
 
+// ------------------------------------------------------------- FP16/FP32
+//
+// The reference's FP16/FP32 GEMV (kernels/gemv/gemv_common.h:1-79):
+// y[n] = sum_k W[n,k] * x[k] accumulated in FP32 and cast once to the
+// dtype of W (RNE for fp16).  W and x are fp16 or fp32, same dtype.
+
+__device__ __forceinline__ float fp_to_f(uint16_t h) { return h2f(h); }
+__device__ __forceinline__ float fp_to_f(float f) { return f; }
+__device__ __forceinline__ void fp_store(uint16_t* p, float v) { *p = f2h(v); }
+__device__ __forceinline__ void fp_store(float* p, float v) { *p = v; }
+
+// One 16-byte chunk of W against the matching chunk of x, into acc, one
+// FMA per element: fp16 operands go straight into v_fma_mix_f32 (the
+// fp16 x fp16 product is exact in FP32, the add is one round-to-nearest-
+// even), fp32 as plain FMAs.  v_dot2_f32_f16 would halve the instructions
+// but measured on gfx950 it is not a single RNE rounding (about 1% of
+// random operands differ from one, in a sign-asymmetric way), and this
+// path is memory-bound at 2 or 4 bytes per element, so the FMA costs
+// nothing.
+__device__ __forceinline__ float fma_pair(uint32_t w, uint32_t x, float acc) {
+    const f16x2 a = as_f16x2(w), b = as_f16x2(x);
+    acc = __builtin_fmaf(static_cast<float>(a[0]), static_cast<float>(b[0]), acc);
+    return __builtin_fmaf(static_cast<float>(a[1]), static_cast<float>(b[1]), acc);
+}
+// Four independent accumulators per lane (one per 32-bit word of a chunk)
+// keep consecutive FMAs free of dependencies; they are summed at the end.
+__device__ __forceinline__ void dot_chunk(uint16_t, const uint4& w,
+                                          const uint4& x, float (&acc)[4]) {
+    acc[0] = fma_pair(w.x, x.x, acc[0]);
+    acc[1] = fma_pair(w.y, x.y, acc[1]);
+    acc[2] = fma_pair(w.z, x.z, acc[2]);
+    acc[3] = fma_pair(w.w, x.w, acc[3]);
+}
+__device__ __forceinline__ void dot_chunk(float, const uint4& w,
+                                          const uint4& x, float (&acc)[4]) {
+    acc[0] = __builtin_fmaf(__builtin_bit_cast(float, w.x), __builtin_bit_cast(float, x.x), acc[0]);
+    acc[1] = __builtin_fmaf(__builtin_bit_cast(float, w.y), __builtin_bit_cast(float, x.y), acc[1]);
+    acc[2] = __builtin_fmaf(__builtin_bit_cast(float, w.z), __builtin_bit_cast(float, x.z), acc[2]);
+    acc[3] = __builtin_fmaf(__builtin_bit_cast(float, w.w), __builtin_bit_cast(float, x.w), acc[3]);
+}
+
+// Scalar: one 256-thread workgroup per row, element loads.  The single
+// source of gemv_baseline and of every fallback (bit-identity of the two).
+template <typename S>
+__global__ __launch_bounds__(kBlock) void gemv_scalar_kernel(
+        const S* __restrict__ w, const S* __restrict__ x, S* __restrict__ y,
+        int64_t k) {
+    const int64_t row = blockIdx.x;
+    const S* __restrict__ wrow = w + row * k;
+    float acc = 0.f;
+    for (int64_t i = threadIdx.x; i < k; i += kBlock)
+        acc = __builtin_fmaf(fp_to_f(wrow[i]), fp_to_f(x[i]), acc);
+    acc = segment_sum<64>(acc);
+    __shared__ float part[kBlock / 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 63) part[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) fp_store(y + row, (part[0] + part[1]) + (part[2] + part[3]));
+}
+
+// Vector: CW lanes per row (64/CW rows per wave), lane `col` owns the
+// 16-byte chunks col + CW*j.  x is staged once per workgroup in LDS
+// ([nchunks + 1] chunks, the last one zero: what lanes past the row end
+// read).  The lane's W chunks stream through two register batches of JB
+// chunks: batch b+1 is in flight while batch b is multiplied, so any K
+// runs with a bounded register budget.
+constexpr int kGemvBatch = 8;
+
+template <typename S, int CW, int NT>
+__global__ __launch_bounds__(NT) void gemv_lds_kernel(
+        const uint4* __restrict__ w,   // [n][nchunks] 16-byte chunks
+        const uint4* __restrict__ x,   // [nchunks] 16-byte chunks
+        S* __restrict__ y, int n, int nchunks) {
+    extern __shared__ uint4 xs[];
+    constexpr int SLOTS = 64 / CW;
+    constexpr int JB = kGemvBatch;
+    constexpr int XB = 4;              // x chunks per thread per staging pass
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int col = lane % CW;
+    const int slot = lane / CW;
+    const uint32_t blk = xcd_contiguous_block();
+    const int64_t row =
+        (static_cast<int64_t>(blk) * (NT >> 6) + (tid >> 6)) * SLOTS + slot;
+    const uint32_t rowc = static_cast<uint32_t>(std::min<int64_t>(row, n - 1));
+    const char* wb = reinterpret_cast<const char*>(w);
+    const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
+    const int nbatch = ((nchunks + CW - 1) / CW + JB - 1) / JB;
+
+    // x first (the barrier waits for it), in passes of XB chunks per thread
+    uint4 xv[XB];
+#pragma unroll
+    for (int i = 0; i < XB; ++i) xv[i] = x[std::min(tid + i * NT, nchunks - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wa[JB], wn[JB];
+    auto load = [&](uint4 (&dst)[JB], int b) {
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+            const int c = col + CW * (b * JB + jj);
+            const uint32_t cl = static_cast<uint32_t>(c < nchunks ? c : nchunks - 1);
+            dst[jj] = *reinterpret_cast<const uint4*>(wb + (rowc * wrow_bytes + cl * 16u));
+        }
+    };
+    load(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < XB; ++i) xs[std::min(tid + i * NT, nchunks - 1)] = xv[i];
+    for (int base = XB * NT; base < nchunks; base += XB * NT) {   // K beyond one pass
+#pragma unroll
+        for (int i = 0; i < XB; ++i) {
+            const int c = std::min(base + tid + i * NT, nchunks - 1);
+            xs[c] = x[c];
+        }
+    }
+    if (tid == 0) xs[nchunks] = uint4{0, 0, 0, 0};
+    __syncthreads();
+
+    float accs[4] = {0.f, 0.f, 0.f, 0.f};
+    auto comp = [&](const uint4 (&src)[JB], int b) {
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+            const int c = col + CW * (b * JB + jj);
+            dot_chunk(S{}, src[jj], xs[c < nchunks ? c : nchunks], accs);
+        }
+    };
+    for (int b = 0; b < nbatch; b += 2) {
+        if (b + 1 < nbatch) load(wn, b + 1);
+        comp(wa, b);
+        if (b + 1 < nbatch) {
+            if (b + 2 < nbatch) load(wa, b + 2);
+            comp(wn, b + 1);
+        }
+    }
+    float acc = (accs[0] + accs[1]) + (accs[2] + accs[3]);
+    acc = segment_sum<CW>(acc);
+    if (col == CW - 1 && row < n) fp_store(y + row, acc);
+}
+
 // ------------------------------------------------- read-only ceiling
 //
 // A plain streaming read of `bytes` (16-byte loads, 4 per thread).  The
@@ -1038,6 +1177,76 @@ hipError_t launch_q8_group(const Plan& p, const GroupProblem* probs,
     return launch_group(instance<Q8LdsGroup<kBlock>>(p.cw, p.j, p.r), p, g, grid,
                         static_cast<uint32_t>(2 * k + 32),
                         static_cast<int>(k / 16), stream);
+}
+
+// ---- FP16/FP32 GEMV
+constexpr int64_t kGemvMaxLdsBytes = 64 * 1024;   // x staged per workgroup
+
+bool gemv_contract_ok(int dtype, const void* w, const void* x, int64_t k) {
+    const int64_t per = dtype == kF32 ? 4 : 8;     // elements per 16 bytes
+    if (k % per != 0) return false;
+    return (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+           (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
+               const void* x) {
+    if (kind == kScalar) return scalar_plan(n, false, "");
+    if (!gemv_contract_ok(dtype, w, x, k))
+        return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k % elements per 16 B)");
+    const int64_t es = dtype == kF32 ? 4 : 2;
+    const int64_t nchunks = k * es / 16;
+    if ((nchunks + 1) * 16 > kGemvMaxLdsBytes)
+        return scalar_plan(n, true, "x above the 64 KiB LDS staging limit");
+    if (n * k * es >= (int64_t{1} << 32))
+        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
+    Plan p;
+    p.kind = kLds;
+    p.cw = pow2_at_least(nchunks, 16);
+    p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
+    p.r = 1;
+    const int64_t waves = (n + (64 / p.cw) - 1) / (64 / p.cw);
+    p.block = kBlock;
+    p.grid = (waves + kBlock / 64 - 1) / (kBlock / 64);
+    return p;
+}
+
+namespace {
+template <typename S>
+using GemvFn = void (*)(const uint4*, const uint4*, S*, int, int);
+
+template <typename S>
+GemvFn<S> gemv_instance(int cw) {
+    if (cw == 16) return &gemv_lds_kernel<S, 16, kBlock>;
+    if (cw == 32) return &gemv_lds_kernel<S, 32, kBlock>;
+    if (cw == 64) return &gemv_lds_kernel<S, 64, kBlock>;
+    return nullptr;
+}
+
+template <typename S>
+hipError_t launch_gemv_t(const Plan& p, const void* w, const void* x, void* y,
+                         int64_t n, int64_t k, hipStream_t stream,
+                         hipEvent_t ev0, hipEvent_t ev1) {
+    if (p.kind == kScalar)
+        return launch(gemv_scalar_kernel<S>, p.grid, p.block, 0, stream, ev0,
+                      ev1, static_cast<const S*>(w), static_cast<const S*>(x),
+                      static_cast<S*>(y), k);
+    const GemvFn<S> fn = gemv_instance<S>(p.cw);
+    if (fn == nullptr) return hipErrorInvalidConfiguration;
+    const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
+    return launch(fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),
+                  stream, ev0, ev1, static_cast<const uint4*>(w),
+                  static_cast<const uint4*>(x), static_cast<S*>(y),
+                  static_cast<int>(n), nchunks);
+}
+}  // namespace
+
+hipError_t launch_gemv(const Plan& p, int dtype, const void* w, const void* x,
+                       void* y, int64_t n, int64_t k, hipStream_t stream,
+                       hipEvent_t ev0, hipEvent_t ev1) {
+    return dtype == kF32
+               ? launch_gemv_t<float>(p, w, x, y, n, k, stream, ev0, ev1)
+               : launch_gemv_t<uint16_t>(p, w, x, y, n, k, stream, ev0, ev1);
 }
 
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

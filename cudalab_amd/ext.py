@@ -388,16 +388,176 @@ class QgemvExt(_OpExt):
                   "(x must be on W_q's device)")
 
 
+class GemvExt(_OpExt):
+    """FP16/FP32 GEMV: W (N,K), x (K,), out (N,), all float16 or all
+    float32; FP32 accumulation (kernels/gemv/gemv_common.h:1-79).
+
+    Same methods as the reference's gemv module
+    (kernels/gemv/bindings.cpp:310-336) with two-tensor signatures:
+    forward(variant, W, x), forward_into(variant, W, x, out),
+    native_timing(variant, W, x, out, ...).  Checks in the order of
+    kernels/gemv/bindings.cpp:87-125."""
+
+    op = "gemv"
+
+    def __init__(self) -> None:
+        super().__init__()
+        self._fn = self._lib.cq_gemv
+        self._grouped_fn = None
+
+    def _w_name(self) -> str:
+        return "W"
+
+    def _k(self, W: torch.Tensor) -> int:
+        return W.size(1)
+
+    @staticmethod
+    def _op_id(W: torch.Tensor) -> int:
+        return (_capi.CQ_OP_GEMV_F32 if W.dtype == torch.float32
+                else _capi.CQ_OP_GEMV_F16)
+
+    def _validate_w(self, W: torch.Tensor) -> None:
+        if W.dim() != 2:
+            _fail(f"W 必须是 2 维 (N, K)，实际 {W.dim()} 维 (W must be 2-D)")
+        if W.size(0) <= 0:
+            _fail(f"N 必须 > 0，实际 {W.size(0)} (N must be > 0)")
+        if W.size(1) <= 0:
+            _fail(f"K 必须 > 0，实际 {W.size(1)} (K must be > 0)")
+        if W.dtype not in (torch.float16, torch.float32):
+            _fail(f"仅支持 float16 / float32，实际 {W.dtype} "
+                  "(only float16 / float32)")
+        if not W.is_contiguous():
+            _fail("W 必须是连续内存 (W must be contiguous)")
+        if not W.is_cuda:
+            _fail("W 必须是 CUDA 张量 (W must be a GPU tensor)")
+
+    def _validate_x(self, W: torch.Tensor, x: torch.Tensor) -> None:
+        if x.dim() != 1:
+            _fail(f"x 必须是 1 维 (K,)，实际 {x.dim()} 维 (x must be 1-D)")
+        if x.size(0) != W.size(1):
+            _fail(f"x 长度必须等于 K: x={x.size(0)} K={W.size(1)} "
+                  "(x length must equal K)")
+        if x.dtype != W.dtype:
+            _fail(f"x 的 dtype 必须与 W 一致: x={x.dtype} W={W.dtype} "
+                  "(x dtype must match W)")
+        if not x.is_contiguous():
+            _fail("x 必须是连续内存 (x must be contiguous)")
+        if not x.is_cuda:
+            _fail("x 必须是 CUDA 张量 (x must be a GPU tensor)")
+        if not _same_device(x, W):
+            _fail("x 必须与 W 在同一 CUDA 设备上 (x must be on W's device)")
+
+    def _validate_out(self, W: torch.Tensor, out: torch.Tensor) -> None:
+        if out.dim() != 1:
+            _fail(f"out 必须是 1 维 (N,)，实际 {out.dim()} 维 (out must be 1-D)")
+        if out.size(0) != W.size(0):
+            _fail(f"out 长度必须等于 N: out={out.size(0)} N={W.size(0)} "
+                  "(out length must equal N)")
+        if out.dtype != W.dtype:
+            _fail(f"out 的 dtype 必须与 W 一致: out={out.dtype} W={W.dtype} "
+                  "(out dtype must match W)")
+        if not out.is_contiguous():
+            _fail("out 必须是连续内存 (out must be contiguous)")
+        if not out.is_cuda:
+            _fail("out 必须是 CUDA 张量 (out must be a GPU tensor)")
+        if not _same_device(out, W):
+            _fail("out 必须与 W 在同一 CUDA 设备上 (out must be on W's device)")
+
+    def _launch2(self, variant: str, W, x, out) -> None:
+        dev = W.device
+        dt = (_capi.CQ_DTYPE_F32 if W.dtype == torch.float32
+              else _capi.CQ_DTYPE_F16)
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = self._fn(variant.encode(), dt, W.data_ptr(), x.data_ptr(),
+                          out.data_ptr(), W.size(0), W.size(1), stream)
+        if st != _capi.CQ_OK:
+            _fail(f"gemv launch failed (status {st}): {_capi.last_error()}")
+
+    def forward(self, variant: str, W: torch.Tensor,  # type: ignore[override]
+                x: torch.Tensor) -> torch.Tensor:
+        """y = W @ x (FP32 accumulation) into a new (N,) tensor of W's dtype."""
+        self._lookup(variant)
+        self._validate_w(W)
+        self._validate_x(W, x)
+        out = torch.empty(W.size(0), dtype=W.dtype, device=W.device)
+        self._launch2(variant, W, x, out)
+        return out
+
+    def forward_into(self, variant: str, W: torch.Tensor,  # type: ignore[override]
+                     x: torch.Tensor, out: torch.Tensor) -> None:
+        self._lookup(variant)
+        self._validate_w(W)
+        self._validate_x(W, x)
+        self._validate_out(W, out)
+        self._launch2(variant, W, x, out)
+
+    def forward_grouped(self, variant, problems):  # type: ignore[override]
+        _fail("gemv 不提供分组调用 (grouped calls exist for int4gemv and qgemv)")
+
+    def native_timing(self, variant: str, W: torch.Tensor,  # type: ignore[override]
+                      x: torch.Tensor, out: torch.Tensor, warmup: int = 200,
+                      n_windows: int = 10,
+                      launches_per_window: int = 64) -> dict:
+        """Native kernel-loop timing (kernels/gemv/bindings.cpp:194-276
+        semantics)."""
+        self._lookup(variant)
+        if warmup < 0:
+            _fail(f"warmup 必须 >= 0，实际 {warmup}")
+        if n_windows < 1:
+            _fail(f"n_windows 必须 >= 1，实际 {n_windows}")
+        if launches_per_window < 1:
+            _fail(f"launches_per_window 必须 >= 1，实际 {launches_per_window}")
+        self._validate_w(W)
+        self._validate_x(W, x)
+        self._validate_out(W, out)
+        win = (ctypes.c_double * n_windows)()
+        res = _capi.CqTiming()
+        dev = W.device
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            st = self._lib.cq_native_timing(
+                self._op_id(W), variant.encode(), W.data_ptr(), None,
+                x.data_ptr(), out.data_ptr(), W.size(0), W.size(1), stream,
+                warmup, n_windows, launches_per_window, win, ctypes.byref(res))
+        if st != _capi.CQ_OK:
+            _fail(f"native_timing failed (status {st}): {_capi.last_error()}")
+        return {
+            "variant": variant,
+            "warmup": int(warmup),
+            "n_windows": int(n_windows),
+            "launches_per_window": int(launches_per_window),
+            "window_median_us": [float(v) for v in win],
+            "median_us": res.median_us,
+            "min_us": res.min_us,
+            "max_us": res.max_us,
+            "mean_us": res.mean_us,
+            "note": NATIVE_TIMING_NOTE,
+        }
+
+    def describe(self, variant: str, W: torch.Tensor, x: torch.Tensor) -> dict:
+        self._lookup(variant)
+        s = _capi._string_call(self._lib.cq_describe_launch, self._op_id(W),
+                               variant.encode(), W.size(0), W.size(1),
+                               W.data_ptr(), x.data_ptr())
+        return _capi.parse_launch_line(s)
+
+    def contract_ok(self, W: torch.Tensor, x: torch.Tensor) -> bool:
+        return bool(self._lib.cq_vec_contract_ok(self._op_id(W), W.data_ptr(),
+                                                 x.data_ptr(), W.size(1)))
+
+
 _EXTS: dict[str, _OpExt] = {}
+_EXT_TYPES = {"int4gemv": Int4gemvExt, "qgemv": QgemvExt, "gemv": GemvExt}
 
 
 def get_ext(op: str) -> _OpExt:
-    """Singleton extension object for "int4gemv" or "qgemv"."""
-    if op not in ("int4gemv", "qgemv"):
+    """Singleton extension object for "int4gemv", "qgemv" or "gemv"."""
+    if op not in _EXT_TYPES:
         raise KeyError(f"no extension for operator {op!r}")
     e = _EXTS.get(op)
     if e is None:
-        e = Int4gemvExt() if op == "int4gemv" else QgemvExt()
+        e = _EXT_TYPES[op]()
         _EXTS[op] = e
     return e
 
@@ -407,26 +567,32 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
                 stream: Optional[torch.cuda.Stream] = None) -> dict:
     """Rotating-pool launch loop in native code (cq_pool_timing).
 
-    `sets` is a list of (W, scale, x, out) tuples of one shape, already
-    validated by the caller.  Returns {"total_us": window event time,
-    "kernel_us": per-launch device durations (list) or None}."""
+    `sets` is a list of (W, scale, x, out) tuples of one shape ((W, x, out)
+    for "gemv"), already validated by the caller.  Returns {"total_us":
+    window event time, "kernel_us": per-launch device durations (list) or
+    None}."""
     lib = _capi.load()
     n = len(sets)
     VP = ctypes.c_void_p * n
+    if op == "gemv":
+        sets = [(W, None, x, o) for (W, x, o) in sets]
     w = VP(*[s[0].data_ptr() for s in sets])
-    sc = VP(*[s[1].data_ptr() for s in sets])
+    sc = VP(*[s[1].data_ptr() for s in sets]) if op != "gemv" else None
     xs = VP(*[s[2].data_ptr() for s in sets])
     ys = VP(*[s[3].data_ptr() for s in sets])
     W0 = sets[0][0]
     N = W0.size(0)
     K = 2 * W0.size(1) if op == "int4gemv" else W0.size(1)
+    op_id = _capi.OPS[op]
+    if op == "gemv":
+        op_id = GemvExt._op_id(W0)
     ku = (ctypes.c_float * n_launches)() if per_kernel else None
     tot = ctypes.c_double(0.0)
     dev = W0.device
     with torch.cuda.device(dev):
         s = stream if stream is not None else torch.cuda.current_stream(dev)
         st = lib.cq_pool_timing(
-            _capi.OPS[op], variant.encode(), w, sc, xs, ys, n, N, K,
+            op_id, variant.encode(), w, sc, xs, ys, n, N, K,
             s.cuda_stream, warmup, n_launches, ku, ctypes.byref(tot))
     if st != _capi.CQ_OK:
         _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")

@@ -21,14 +21,20 @@
  *     y     f16 [n]
  *     Wdequant[n,k] = w_q[n,k] * scale[n]; any k >= 1.
  *
+ *   gemv (FP16 / FP32, the reference's third generation):
+ *     w  f16 or f32 [n, k] row-major
+ *     x  same dtype [k]
+ *     y  same dtype [n]
+ *     y[n] = sum_k w[n,k] * x[k] in FP32, cast once to the dtype.
+ *
  * All pointers are device pointers on the current HIP device; `stream` is a
  * hipStream_t (NULL = the null stream).  Calls are asynchronous: a kernel is
  * enqueued and the call returns.  The library never allocates device memory
  * on these paths and keeps no state between calls.
  *
  * Vector contract (checked on the host before every launch): the vectorized
- * kernels need w and x 16-byte aligned and k % 32 == 0 (int4gemv) or
- * k % 16 == 0 (qgemv).  Inputs that miss it are never rejected: they run on
+ * kernels need w and x 16-byte aligned and k % 32 == 0 (int4gemv),
+ * k % 16 == 0 (qgemv), k % 8 == 0 (gemv fp16) or k % 4 == 0 (gemv fp32).  Inputs that miss it are never rejected: they run on
  * the scalar kernel of the `*_baseline` variant, so their output is
  * bit-identical to that variant's.
  *
@@ -56,9 +62,16 @@ extern "C" {
 #define CQ_ERR_HIP              3
 #define CQ_ERR_BUFFER_TOO_SMALL 4
 
-/* operator ids */
+/* operator ids (the timing, list and describe entry points take these;
+ * gemv has one id per dtype and one shared variant registry) */
 #define CQ_OP_INT4GEMV 0
 #define CQ_OP_QGEMV    1
+#define CQ_OP_GEMV_F16 2
+#define CQ_OP_GEMV_F32 3
+
+/* gemv element types */
+#define CQ_DTYPE_F16 0
+#define CQ_DTYPE_F32 1
 
 /* variant list selectors */
 #define CQ_LIST_NORMAL      0
@@ -85,6 +98,15 @@ int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
  */
 int cq_qgemv(const char* variant, const void* w_q, const void* scale,
              const void* x, void* y, int64_t n, int64_t k, void* stream);
+
+/*
+ * One FP16 or FP32 GEMV launch: y = w @ x, FP32 accumulation, y in the
+ * dtype of w (dtype = CQ_DTYPE_F16 or CQ_DTYPE_F32).  Replaces `gemv_fn_t`
+ * (kernels/gemv/gemv_common.h:53-55) behind `gemv_forward` /
+ * `gemv_forward_into` (kernels/gemv/bindings.cpp:137-190).
+ */
+int cq_gemv(const char* variant, int dtype, const void* w, const void* x,
+            void* y, int64_t n, int64_t k, void* stream);
 
 /* One problem of a grouped call: device pointers and its row count. */
 typedef struct cq_gemv_problem {

@@ -18,6 +18,12 @@ the reference repository).  How each is pinned (tests/test_oracle_*.py):
   arith_ratio             the bound of cudalab/int4gemv_correctness.py:
                           175-209; planted mistakes (nibble swap, lost sign
                           extension, wrong group, dropped term) exceed it
+  exact_gemv              Fraction arithmetic on small fp16/fp32 inputs,
+                          one-hot and constant closed forms
+  arith_ratio_gemv        the bound of cudalab/gemv_correctness.py:175-200;
+                          planted mistakes (transposed W, dropped term,
+                          fp16 accumulation) exceed it
+  ulp32                   numpy.spacing on float32
 """
 from __future__ import annotations
 
@@ -65,6 +71,9 @@ def lib():
         L.orc_unpack_bytes.argtypes = [P, i64, P]
         L.orc_int4_gemv_cpu.argtypes = [P, P, P, P, i64, i64, ctypes.c_int, P]
         L.orc_q8_gemv_cpu.argtypes = [P, P, P, P, i64, i64, ctypes.c_int, P]
+        L.orc_gemv_exact.argtypes = [ctypes.c_int, P, P, i64, i64, P, P]
+        L.orc_gemv_exact.restype = ctypes.c_int
+        L.orc_gemv_cpu.argtypes = [ctypes.c_int, P, P, P, i64, i64, ctypes.c_int, P]
         L.orc_f2h.argtypes = [ctypes.c_float]
         L.orc_f2h.restype = ctypes.c_uint16
         L.orc_h2d.argtypes = [ctypes.c_uint16]
@@ -250,6 +259,76 @@ def arith_ratio(y16: np.ndarray, exact: np.ndarray, S: np.ndarray,
     with np.errstate(invalid="ignore"):
         r = diff / tol
     return np.where(np.isfinite(r), r, np.inf)
+
+
+# ------------------------------------------------ FP16 / FP32 GEMV
+
+def _gemv_dtype(a: np.ndarray) -> int:
+    if a.dtype == np.float16:
+        return 0
+    if a.dtype == np.float32:
+        return 1
+    raise TypeError(f"gemv oracle takes float16 or float32, got {a.dtype}")
+
+
+def exact_gemv(W: np.ndarray, x: np.ndarray):
+    """(exact, S) per row of the FP16/FP32 GEMV W @ x: fp16 in exact
+    integer arithmetic, fp32 as exact products in double-double."""
+    W = np.ascontiguousarray(W)
+    x = np.ascontiguousarray(x)
+    dt = _gemv_dtype(W)
+    if x.dtype != W.dtype:
+        raise TypeError("x and W must share a dtype")
+    N, K = W.shape
+    ex = np.empty(N, dtype=np.float64)
+    S = np.empty(N, dtype=np.float64)
+    lib().orc_gemv_exact(dt, _p(W), _p(x), N, K, _p(ex), _p(S))
+    return ex, S
+
+
+def ulp32(v: np.ndarray) -> np.ndarray:
+    """float32 grid spacing at |v| (nextafter toward +inf minus v, as
+    cudalab/gemv_correctness.py:_ulp does for float32)."""
+    a = np.abs(np.asarray(v, dtype=np.float64).astype(np.float32))
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (np.nextafter(a, np.float32(np.inf)) - a).astype(np.float64)
+
+
+GEMV_TERM_ROUNDINGS = 2.0
+
+
+def arith_ratio_gemv(y: np.ndarray, exact: np.ndarray, S: np.ndarray,
+                     K: int, dtype) -> np.ndarray:
+    """Per-row |y - exact| / tol with
+    tol = TOL_K * (2*K*2^-24*S + ulp(y)/2 + ulp(exact)/2) on the grid of
+    `dtype` (cudalab/gemv_correctness.py:175-200); non-finite -> inf."""
+    dt = np.dtype(dtype)
+    ulp = ulp16 if dt == np.float16 else ulp32
+    yd = np.asarray(y).astype(dt).astype(np.float64)
+    tol = TOL_K * (GEMV_TERM_ROUNDINGS * K * 2.0 ** -24 * S
+                   + 0.5 * ulp(yd) + 0.5 * ulp(exact))
+    diff = np.abs(yd - exact)
+    with np.errstate(invalid="ignore"):
+        r = diff / tol
+    return np.where(np.isfinite(r), r, np.inf)
+
+
+def check_gemv(y, W, x) -> float:
+    ex, S = exact_gemv(W, x)
+    r = arith_ratio_gemv(y, ex, S, np.asarray(W).shape[1], np.asarray(W).dtype)
+    return float(r.max()) if r.size else 0.0
+
+
+def gemv_cpu(W: np.ndarray, x: np.ndarray, threads: int | None = None) -> np.ndarray:
+    """Fused OpenMP CPU FP16/FP32 GEMV, FP32 accumulation."""
+    W = np.ascontiguousarray(W)
+    x = np.ascontiguousarray(x)
+    dt = _gemv_dtype(W)
+    N, K = W.shape
+    y = np.empty(N, dtype=W.dtype)
+    xf = np.empty(K, dtype=np.float32)
+    lib().orc_gemv_cpu(dt, _p(W), _p(x), _p(y), N, K, threads or max_threads(), _p(xf))
+    return y
 
 
 def check_w4(y16, wp, scale, x) -> float:

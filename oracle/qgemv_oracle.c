@@ -22,6 +22,15 @@
  *   orc_q8_ref_f32      cudalab/qgemv_correctness.py:189-190, likewise
  *   orc_int4_gemv_cpu   the same FP32 computation as a fused, row-parallel
  *   orc_q8_gemv_cpu     CPU kernel (OpenMP), for the CPU baseline timing
+ *   orc_gemv_exact      the fp64 "exact" and S_n of the FP16/FP32 GEMV
+ *                       bound (cudalab/gemv_correctness.py:175-200): fp16
+ *                       in exact integer arithmetic (one rounding), fp32
+ *                       as exact products summed in double-double
+ *                       (relative error ~ K * 2^-106, far below the bound)
+ *   orc_gemv_cpu        FP16/FP32 GEMV, FP32 accumulation, row-parallel
+ *                       (OpenMP), the reference's gemv_ref formulation
+ *                       torch.mv(W.float(), x.float()) (operators/gemv.py:
+ *                       192-200) for the CPU baseline timing
  *
  * Exact arithmetic: every fp16 value is an integer multiple of 2^-24 with
  * magnitude below 2^40 (in units of 2^-24).  An INT4 term q*s*x is then an
@@ -314,6 +323,109 @@ void orc_q8_gemv_cpu(const int8_t* wq, const float* scale, const uint16_t* x,
         float t = 0.f;
         for (int l = 0; l < ORC_LANES; ++l) t = t + acc[l];
         y[r] = orc_f2h(scale[r] * t);
+    }
+}
+
+/* ---- FP16 / FP32 GEMV ---------------------------------------------- */
+
+/* Error-free sum a + b = s + e (Knuth's TwoSum). */
+static void two_sum(double a, double b, double* s, double* e) {
+    const double t = a + b;
+    const double bb = t - a;
+    *e = (a - (t - bb)) + (b - bb);
+    *s = t;
+}
+
+/* dtype 0: w, x fp16 bits; dtype 1: w, x float32.  exact[n] = sum_k w*x,
+ * S[n] = sum_k |w*x|.  Returns 0, or -1 if an input is inf/nan (then the
+ * affected rows get NaN). */
+int orc_gemv_exact(int dtype, const void* w, const void* x, int64_t n,
+                   int64_t k, double* exact, double* S) {
+    int bad = 0;
+    if (dtype == 0) {
+        const uint16_t* wh = (const uint16_t*)w;
+        const uint16_t* xh = (const uint16_t*)x;
+        for (int64_t r = 0; r < n; ++r) {
+            i128 sum = 0, abs_sum = 0;
+            int row_bad = 0;
+            for (int64_t i = 0; i < k; ++i) {
+                int64_t mw, mx;
+                if (!h_fixed(wh[r * k + i], &mw) || !h_fixed(xh[i], &mx)) {
+                    row_bad = 1;
+                    continue;
+                }
+                const i128 t = (i128)mw * (i128)mx;   /* value * 2^48 */
+                sum += t;
+                abs_sum += t < 0 ? -t : t;
+            }
+            if (row_bad) {
+                exact[r] = S[r] = NAN;
+                bad = 1;
+                continue;
+            }
+            exact[r] = ldexp((double)sum, -48);
+            S[r] = ldexp((double)abs_sum, -48);
+        }
+        return bad ? -1 : 0;
+    }
+    const float* wf = (const float*)w;
+    const float* xf = (const float*)x;
+    for (int64_t r = 0; r < n; ++r) {
+        double hi = 0.0, lo = 0.0, ahi = 0.0, alo = 0.0;
+        int row_bad = 0;
+        for (int64_t i = 0; i < k; ++i) {
+            const float a = wf[r * k + i], b = xf[i];
+            if (!isfinite(a) || !isfinite(b)) {
+                row_bad = 1;
+                continue;
+            }
+            const double t = (double)a * (double)b;   /* exact: 24 + 24 bits */
+            double s1, e1;
+            two_sum(hi, t, &s1, &e1);
+            hi = s1;
+            lo += e1;
+            two_sum(ahi, fabs(t), &s1, &e1);
+            ahi = s1;
+            alo += e1;
+        }
+        if (row_bad) {
+            exact[r] = S[r] = NAN;
+            bad = 1;
+            continue;
+        }
+        exact[r] = hi + lo;
+        S[r] = ahi + alo;
+    }
+    return bad ? -1 : 0;
+}
+
+void orc_gemv_cpu(int dtype, const void* w, const void* x, void* y, int64_t n,
+                  int64_t k, int threads, float* xf) {
+    const uint16_t* wh = (const uint16_t*)w;
+    const float* wf = (const float*)w;
+    for (int64_t i = 0; i < k; ++i)
+        xf[i] = dtype == 0 ? h2f(((const uint16_t*)x)[i]) : ((const float*)x)[i];
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (int64_t r = 0; r < n; ++r) {
+        float acc[ORC_LANES] = {0};
+        int64_t i = 0;
+        if (dtype == 0) {
+            const uint16_t* row = wh + r * k;
+            for (; i + ORC_LANES <= k; i += ORC_LANES)
+                for (int l = 0; l < ORC_LANES; ++l)
+                    acc[l] = acc[l] + h2f(row[i + l]) * xf[i + l];
+            for (; i < k; ++i) acc[0] = acc[0] + h2f(row[i]) * xf[i];
+        } else {
+            const float* row = wf + r * k;
+            for (; i + ORC_LANES <= k; i += ORC_LANES)
+                for (int l = 0; l < ORC_LANES; ++l)
+                    acc[l] = acc[l] + row[i + l] * xf[i + l];
+            for (; i < k; ++i) acc[0] = acc[0] + row[i] * xf[i];
+        }
+        float t = 0.f;
+        for (int l = 0; l < ORC_LANES; ++l) t = t + acc[l];
+        if (dtype == 0) ((uint16_t*)y)[r] = orc_f2h(t);
+        else ((float*)y)[r] = t;
     }
 }
 

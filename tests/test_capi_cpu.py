@@ -27,7 +27,7 @@ def _declared_functions() -> set[str]:
 def test_header_declares_the_abi():
     names = _declared_functions()
     assert {"cq_int4gemv", "cq_qgemv", "cq_native_timing", "cq_pool_timing", "cq_read_ceiling",
-            "cq_int4gemv_grouped", "cq_qgemv_grouped",
+            "cq_int4gemv_grouped", "cq_qgemv_grouped", "cq_gemv",
             "cq_variants", "cq_vec_contract_ok", "cq_describe_launch",
             "cq_last_error", "cq_version"} <= names
 
@@ -174,3 +174,38 @@ def test_grouped_argument_errors_without_launch():
     probs[2].n = 0
     st = lib.cq_qgemv_grouped(b"qgemv_cdna4", probs, 3, 16, None)
     assert st == _capi.CQ_ERR_INVALID_ARG and _capi.last_error().startswith("problem 2:")
+
+
+
+@pytest.mark.parametrize("op,n,k,kernel,cw,j", [
+    ("gemv_f16", 4096, 4096, "lds", 64, 8),
+    ("gemv_f32", 4096, 4096, "lds", 64, 16),
+    ("gemv_f16", 4096, 11008, "lds", 64, 22),
+    ("gemv_f32", 11008, 4096, "lds", 64, 16),
+    ("gemv_f16", 7, 64, "lds", 16, 1),
+    ("gemv_f32", 4096, 16384, "scalar", 0, 0),    # x above the LDS limit
+    ("gemv_f16", 16, 13, "scalar", 0, 0),         # K % 8 != 0
+])
+def test_gemv_launch_plans(op, n, k, kernel, cw, j):
+    d = _capi.describe_launch(op, "gemv_cdna4", n, k, 4096, 8192)
+    assert (d["kernel"], int(d["cw"]), int(d["j"])) == (kernel, cw, j)
+    if kernel == "lds":
+        assert d["fallback"] == "0" and int(d["block"]) == 256
+        assert int(d["grid"]) == -(-n // ((64 // cw) * 4))
+    else:
+        assert d["fallback"] == "1"
+
+
+def test_gemv_argument_errors_without_launch():
+    lib = _capi.load()
+    P = 0x1000
+    assert lib.cq_gemv(b"gemv_cdna4", 2, P, P, P, 4, 8, None) == _capi.CQ_ERR_INVALID_ARG
+    assert "dtype" in _capi.last_error()
+    assert lib.cq_gemv(b"nope", 0, P, P, P, 4, 8, None) == _capi.CQ_ERR_UNKNOWN_VARIANT
+    assert lib.cq_gemv(b"gemv_cdna4", 0, None, P, P, 4, 8, None) == _capi.CQ_ERR_INVALID_ARG
+    assert lib.cq_gemv(b"gemv_cdna4", 1, P, P, P, 4, 0, None) == _capi.CQ_ERR_INVALID_ARG
+    # the gemv registry is shared by both dtype ids
+    assert _capi.variant_list("gemv_f32", _capi.CQ_LIST_ALL) == \
+        _capi.variant_list("gemv_f16", _capi.CQ_LIST_ALL)
+    assert _capi.vec_contract_ok("gemv_f32", 0x1000, 0x2000, 12)
+    assert not _capi.vec_contract_ok("gemv_f16", 0x1000, 0x2000, 12)

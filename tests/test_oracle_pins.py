@@ -324,3 +324,72 @@ def test_gate_rejects_planted_mistakes():
     xp[:32], xp[32:64] = x[32:64], x[:32]
     y = _y_sequential(q, s, xp)
     assert orc.check_w4(y, wp, s, x) > 1.0
+
+
+# ------------------------------------------------ FP16 / FP32 GEMV oracle
+
+def _fp_inputs(rng, N, K, dt, scales=(1e-6, 1.0, 300.0)):
+    W = (rng.standard_normal((N, K)) * rng.choice(scales, (N, K))).astype(dt)
+    x = (rng.standard_normal(K) * rng.choice(scales, K)).astype(dt)
+    return W, x
+
+
+@pytest.mark.parametrize("dt", [np.float16, np.float32])
+@pytest.mark.parametrize("N,K", [(3, 1), (5, 37), (4, 129)])
+def test_exact_gemv_matches_fractions(dt, N, K):
+    rng = np.random.default_rng(N * 1000 + K)
+    W, x = _fp_inputs(rng, N, K, dt)
+    ex, S = orc.exact_gemv(W, x)
+    for r in range(N):
+        terms = [Fraction(float(W[r, k])) * Fraction(float(x[k])) for k in range(K)]
+        assert float(sum(terms)) == ex[r]
+        assert float(sum(abs(t) for t in terms)) == S[r]
+
+
+def test_exact_gemv_closed_forms():
+    rng = np.random.default_rng(5)
+    for dt in (np.float16, np.float32):
+        W = rng.standard_normal((6, 40)).astype(dt)
+        for j in (0, 17, 39):                       # one-hot x picks a column
+            x = np.zeros(40, dtype=dt)
+            x[j] = 1
+            ex, S = orc.exact_gemv(W, x)
+            assert np.array_equal(ex, W[:, j].astype(np.float64))
+            assert np.array_equal(S, np.abs(W[:, j]).astype(np.float64))
+        ones = np.ones(40, dtype=dt)                # all-ones x sums the rows
+        ex, _ = orc.exact_gemv(np.ones((2, 40), dtype=dt), ones)
+        assert np.array_equal(ex, np.full(2, 40.0))
+    # fp16 subnormal products stay exact (2^-24 * 2^-24 = 2^-48)
+    t = np.array([[2.0 ** -24] * 8], dtype=np.float16)
+    ex, _ = orc.exact_gemv(t, np.full(8, 2.0 ** -24, dtype=np.float16))
+    assert ex[0] == 8 * 2.0 ** -48
+
+
+def test_ulp32_matches_spacing():
+    v = np.array([0.0, 1e-45, 1.0, 3.5, 1e30, -2.0, 65504.0], dtype=np.float32)
+    assert np.array_equal(orc.ulp32(v), np.spacing(np.abs(v)).astype(np.float64))
+
+
+@pytest.mark.parametrize("dt", [np.float16, np.float32])
+def test_gemv_gate_accepts_cpu_gemv_and_rejects_planted_mistakes(dt):
+    rng = np.random.default_rng(11)
+    N, K = 64, 1024
+    W = rng.standard_normal((N, K)).astype(dt)
+    x = rng.standard_normal(K).astype(dt)
+    ex, S = orc.exact_gemv(W, x)
+    y = orc.gemv_cpu(W, x, threads=2)
+    assert orc.arith_ratio_gemv(y, ex, S, K, dt).max() <= 1.0
+    # a dropped term (the last column) is far outside the bound
+    y_drop = (W[:, :-1].astype(np.float64) @ x[:-1].astype(np.float64)).astype(dt)
+    assert orc.arith_ratio_gemv(y_drop, ex, S, K, dt).max() > 1.0
+    # the transposed operand (W^T of a square block)
+    Wsq = W[:, :N]
+    exq, Sq = orc.exact_gemv(np.ascontiguousarray(Wsq), x[:N].copy())
+    y_t = (Wsq.T.astype(np.float64) @ x[:N].astype(np.float64)).astype(dt)
+    assert orc.arith_ratio_gemv(y_t, exq, Sq, N, dt).max() > 1.0
+    if dt == np.float16:
+        # accumulating in fp16 instead of FP32 breaks the bound
+        acc = np.zeros(N, dtype=np.float16)
+        for k in range(K):
+            acc = (acc + W[:, k] * x[k]).astype(np.float16)
+        assert orc.arith_ratio_gemv(acc, ex, S, K, dt).max() > 1.0

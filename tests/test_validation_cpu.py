@@ -127,7 +127,7 @@ def test_registry_api(e4, e8):
     assert e4.resolve("int4gemv_rowtile4_hx") == "int4gemv_cdna4"
     assert e8.resolve("qgemv_vec16_row") == "qgemv_cdna4"
     from cudalab_amd.operators import get, names
-    assert names() == ["int4gemv", "qgemv"]
+    assert names() == ["gemv", "int4gemv", "qgemv"]
     assert get("int4gemv").variants(e4) == e4.variants()
     with pytest.raises(KeyError):
         get("rmsnorm")
@@ -145,3 +145,47 @@ def test_grouped_checks(e4, monkeypatch):
         monkeypatch.setattr(type(e4), name, lambda self, *a: None)
     W2 = torch.zeros(8, 256, dtype=torch.uint8)
     assert "share K" in _msg(lambda: e4.forward_grouped("int4gemv_cdna4", [(W, s, x, o), (W2, s, x, o)]))
+
+
+@pytest.fixture(scope="module")
+def eg():
+    return build("gemv")
+
+
+def test_gemv_cases_in_reference_order(eg, monkeypatch):
+    """kernels/gemv/bindings.cpp:87-125: W dim, N, K, dtype, contiguous,
+    device; then x; then out."""
+    W = torch.zeros(8, 64, dtype=torch.float16)
+    x = torch.zeros(64, dtype=torch.float16)
+    f = lambda *a: eg.forward("gemv_cdna4", *a)  # noqa: E731
+    assert "必须是 2 维" in _msg(lambda: f(W.view(-1), x))
+    assert "N 必须 > 0" in _msg(lambda: f(torch.zeros(0, 64, dtype=torch.float16), x))
+    assert "K 必须 > 0" in _msg(lambda: f(torch.zeros(8, 0, dtype=torch.float16), x))
+    assert "float16 / float32" in _msg(lambda: f(W.bfloat16(), x))
+    assert "float16 / float32" in _msg(lambda: f(W.int(), x))
+    assert "连续内存" in _msg(lambda: f(torch.zeros(64, 8, dtype=torch.float16).t(), x))
+    assert "CUDA 张量" in _msg(lambda: f(W, x))
+    assert "未知 gemv 变体" in _msg(lambda: eg.forward("zzz", W, x))
+    m = _msg(lambda: eg.forward("zzz", W, x))
+    assert "gemv_splitk4" in m and "NOT_FOR_NORMAL_DISPATCH" in m
+    monkeypatch.setattr(type(eg), "_validate_w", lambda self, Wa: None)
+    assert "必须是 1 维" in _msg(lambda: f(W, x.view(1, -1)))
+    assert "x 长度必须等于 K" in _msg(lambda: f(W, x[:63].contiguous()))
+    assert "dtype 必须与 W 一致" in _msg(lambda: f(W, x.float()))
+    assert "连续内存" in _msg(lambda: f(W, torch.zeros(128, dtype=torch.float16)[::2]))
+    assert "CUDA 张量" in _msg(lambda: f(W, x))
+    monkeypatch.setattr(type(eg), "_validate_x", lambda self, Wa, xa: None)
+    g = lambda o: eg.forward_into("gemv_cdna4", W, x, o)  # noqa: E731
+    assert "out 长度必须等于 N" in _msg(lambda: g(torch.zeros(7, dtype=torch.float16)))
+    assert "必须是 1 维" in _msg(lambda: g(torch.zeros(8, 1, dtype=torch.float16)))
+    assert "dtype 必须与 W 一致" in _msg(lambda: g(torch.zeros(8)))
+    assert "连续内存" in _msg(lambda: g(torch.zeros(16, dtype=torch.float16)[::2]))
+    assert "CUDA 张量" in _msg(lambda: g(torch.zeros(8, dtype=torch.float16)))
+
+
+def test_gemv_registry(eg):
+    assert eg.variants() == ["gemv_baseline", "gemv_cdna4"]
+    assert eg.quarantined_variants() == ["gemv_splitk4"]
+    assert eg.all_variants() == ["gemv_baseline", "gemv_cdna4", "gemv_splitk4"]
+    assert eg.resolve("gemv_vec4_row") == "gemv_cdna4"
+    assert eg.resolve("gemv_warp_vec4") == "gemv_cdna4"
