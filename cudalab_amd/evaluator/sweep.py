@@ -1,8 +1,8 @@
 """Shape sweep of the GEMV path on one GPU: µs per call, effective GB/s,
-fraction of HBM peak and of the measured read ceiling, for INT4 and INT8
-over the reference's five bench shapes (cudalab/operators/int4gemv.py:30-36
-lists the same matrix) in streaming (HBM-cold pool) and hot (one resident
-set) modes.
+fraction of HBM peak and of the measured read ceiling, for the three
+generations INT4, INT8 and FP16 over the reference's five bench shapes
+(cudalab/operators/int4gemv.py:30-36 lists the same matrix) in streaming
+(HBM-cold pool) and hot (one resident set) modes.
 
 Timing caliber: K back-to-back launches on one stream between two HIP
 events (cq_pool_timing), the same as bench.py's headline.  The read
@@ -25,22 +25,29 @@ from .bench import cold_pool_sets
 HBM_PEAK_GBS = 8000.0
 SHAPES = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
           (4096, 11008)]
-OPS = {"int4gemv": "int4gemv_cdna4", "qgemv": "qgemv_cdna4"}
+OPS = {"int4gemv": "int4gemv_cdna4", "qgemv": "qgemv_cdna4",
+       "gemv": "gemv_cdna4"}
 
 
 def algorithmic_bytes(op: str, N: int, K: int) -> int:
     if op == "int4gemv":
         from ..operators.int4gemv import int4_bytes
         return int4_bytes(N, K)
+    if op == "gemv":
+        from ..operators.gemv import gemv_bytes
+        return gemv_bytes(N, K, 2)
     from ..operators.qgemv import q8_bytes
     return q8_bytes(N, K)
 
 
 def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
     """Input sets drawn on the device: a pool of more than 512 MiB of
-    distinct sets for "streaming", one set for "hot"."""
+    distinct sets for "streaming", one set for "hot".  INT4/INT8 sets are
+    (W, scale, x, out); FP16 sets are (W, x, out)."""
     if op == "int4gemv":
         from ..operators.int4gemv import device_random_set
+    elif op == "gemv":
+        from ..operators.gemv import device_random_set
     else:
         from ..operators.qgemv import device_random_set
     nbytes = algorithmic_bytes(op, N, K)
@@ -65,7 +72,8 @@ def run(ops=tuple(OPS), shapes=SHAPES, modes=("streaming", "hot"),
         for (N, K) in shapes:
             for mode in modes:
                 sets, nbytes = make_sets(op, N, K, mode)
-                plan = ext.describe(variant, sets[0][0], sets[0][2])
+                x0 = sets[0][1] if op == "gemv" else sets[0][2]
+                plan = ext.describe(variant, sets[0][0], x0)
                 us = window_us(op, variant, sets, steps, warmup)
                 rec = {"op": op, "variant": variant, "N": N, "K": K,
                        "mode": mode, "pool_sets": len(sets),
@@ -98,17 +106,39 @@ def table(records: list[dict]) -> str:
     return "\n".join(lines)
 
 
+def speedups(records: list[dict]) -> str:
+    """INT4 vs INT8 vs FP16 per shape and mode (µs ratios)."""
+    by = {(r["op"], r["N"], r["K"], r["mode"]): r["us_per_call"] for r in records}
+    lines = [f"{'N':>6} {'K':>6} {'mode':<9} {'int4 us':>8} {'int8 us':>8} "
+             f"{'fp16 us':>8} {'int8/int4':>9} {'fp16/int4':>9}"]
+    for (op, N, K, mode), us in by.items():
+        if op != "int4gemv":
+            continue
+        q8, f16 = by.get(("qgemv", N, K, mode)), by.get(("gemv", N, K, mode))
+        if q8 is None or f16 is None:
+            continue
+        lines.append(f"{N:>6} {K:>6} {mode:<9} {us:>8.3f} {q8:>8.3f} {f16:>8.3f} "
+                     f"{q8 / us:>9.3f} {f16 / us:>9.3f}")
+    return "\n".join(lines)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--ops", default=",".join(OPS))
     ap.add_argument("--json", default=None)
     a = ap.parse_args(argv)
+    ops = tuple(o for o in a.ops.split(",") if o)
+    if not ops or any(o not in OPS for o in ops):
+        print(f"sweep: --ops must name some of {tuple(OPS)}", file=sys.stderr)
+        return 2
     if not torch.cuda.is_available():
         print("sweep: no GPU visible", file=sys.stderr)
         return 1
-    recs = run(steps=a.steps, warmup=a.warmup)
+    recs = run(ops=ops, steps=a.steps, warmup=a.warmup)
     print(table(recs), flush=True)
+    print("\n" + speedups(recs), flush=True)
     if a.json:
         with open(a.json, "w") as f:
             json.dump(recs, f, indent=1)
