@@ -31,6 +31,11 @@ CQ_OP_GEMV_F32 = 3
 CQ_DTYPE_F16 = 0
 CQ_DTYPE_F32 = 1
 
+# quantizer scale forms: amax / qmax (torch on the CPU) or amax * fl(1/qmax)
+# (torch on a GPU)
+CQ_SCALE_DIV = 0
+CQ_SCALE_RCP = 1
+
 CQ_LIST_NORMAL = 0
 CQ_LIST_ALL = 1
 CQ_LIST_QUARANTINED = 2
@@ -79,6 +84,12 @@ SIGNATURES = {
                                            _i64, _i64, _vp]),
     "cq_qgemv_grouped": (ctypes.c_int, [_cstr, ctypes.POINTER(CqProblem),
                                         _i64, _i64, _vp]),
+    "cq_int4_quantize": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64,
+                                        ctypes.c_int, _vp]),
+    "cq_q8_quantize": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64,
+                                      ctypes.c_int, _vp]),
+    "cq_quantize_vectorized": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64,
+                                              _i64]),
     "cq_native_timing": (ctypes.c_int, [
         ctypes.c_int, _cstr, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
         _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(CqTiming)]),

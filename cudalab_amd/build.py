@@ -36,7 +36,7 @@ LIB_NAME = "libcdnaqgemv.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 
 ARCH = "gfx950"
-SOURCES = ("cq_kernels.hip", "cq_capi.cpp")
+SOURCES = ("cq_kernels.hip", "cq_quantize.hip", "cq_capi.cpp")
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",

@@ -185,6 +185,28 @@ int run_one(int op, const char* variant, const void* w, const void* scale,
     return CQ_OK;
 }
 
+// Argument checks of the quantizer entry points (plain pointers and sizes;
+// the Python layer keeps the reference's ValueError checks on metadata).
+int check_quantize(int op, const void* w, const void* q, const void* scale,
+                   int64_t n, int64_t k, int scale_mode) {
+    if (scale_mode != CQ_SCALE_DIV && scale_mode != CQ_SCALE_RCP)
+        return fail(CQ_ERR_INVALID_ARG, "unknown scale_mode " + std::to_string(scale_mode));
+    if (w == nullptr || q == nullptr || scale == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null pointer argument");
+    if (n < 1 || k < 1 || n > INT_MAX || k > INT_MAX)
+        return fail(CQ_ERR_INVALID_ARG, "n and k must be in [1, INT_MAX] (n=" +
+                                            std::to_string(n) + ", k=" + std::to_string(k) + ")");
+    if (op == CQ_OP_INT4GEMV && k % 128 != 0)
+        return fail(CQ_ERR_INVALID_ARG, "k must be divisible by 128 (got k=" +
+                                            std::to_string(k) + ")");
+    const uintptr_t sa = op == CQ_OP_INT4GEMV ? 2 : 4;
+    if ((reinterpret_cast<uintptr_t>(w) & 1u) != 0 ||
+        reinterpret_cast<uintptr_t>(scale) % sa != 0)
+        return fail(CQ_ERR_INVALID_ARG, "w must be 2-byte aligned and scale aligned "
+                                        "to its element size");
+    return CQ_OK;
+}
+
 int run_grouped(int op, const char* variant, const cq_gemv_problem_t* probs,
                 int64_t count, int64_t k, void* stream) {
     g_last_error.clear();
@@ -294,6 +316,40 @@ int cq_int4gemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
 int cq_qgemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
                      int64_t n_problems, int64_t k, void* stream) {
     return run_grouped(CQ_OP_QGEMV, variant, problems, n_problems, k, stream);
+}
+
+int cq_int4_quantize(const void* w, void* w_packed, void* scale, int64_t n,
+                     int64_t k, int scale_mode, void* stream) {
+    g_last_error.clear();
+    int st = check_quantize(CQ_OP_INT4GEMV, w, w_packed, scale, n, k, scale_mode);
+    if (st != CQ_OK) return st;
+    const cq::QuantPlan p = cq::plan_int4_quantize(n, k, w, w_packed);
+    if (p.grid > INT_MAX) return fail(CQ_ERR_INVALID_ARG, "n * k too large for one launch");
+    const hipError_t e = cq::launch_int4_quantize(p, w, w_packed, scale, n, k,
+                                                  scale_mode == CQ_SCALE_RCP,
+                                                  static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return CQ_OK;
+}
+
+int cq_q8_quantize(const void* w, void* w_q, void* scale, int64_t n, int64_t k,
+                   int scale_mode, void* stream) {
+    g_last_error.clear();
+    int st = check_quantize(CQ_OP_QGEMV, w, w_q, scale, n, k, scale_mode);
+    if (st != CQ_OK) return st;
+    const cq::QuantPlan p = cq::plan_q8_quantize(n, k, w, w_q);
+    const hipError_t e = cq::launch_q8_quantize(p, w, w_q, scale, n, k,
+                                                scale_mode == CQ_SCALE_RCP,
+                                                static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return CQ_OK;
+}
+
+int cq_quantize_vectorized(int op, const void* w, const void* out, int64_t n,
+                           int64_t k) {
+    if (op == CQ_OP_INT4GEMV) return cq::plan_int4_quantize(n, k, w, out).fast ? 1 : 0;
+    if (op == CQ_OP_QGEMV) return cq::plan_q8_quantize(n, k, w, out).fast ? 1 : 0;
+    return fail(CQ_ERR_INVALID_ARG, "quantizers exist for CQ_OP_INT4GEMV and CQ_OP_QGEMV only"), -1;
 }
 
 int cq_native_timing(int op, const char* variant, const void* w,

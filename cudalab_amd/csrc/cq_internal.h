@@ -83,6 +83,25 @@ hipError_t launch_gemv(const Plan& plan, int dtype, const void* w,
                        const void* x, void* y, int64_t n, int64_t k,
                        hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
 
+// On-device weight quantizers (INT4 group-wise with packing, INT8 per row).
+// `fast` selects the vectorized kernel (alignment and k permitting); the
+// generic kernel evaluates the same definition element by element.
+struct QuantPlan {
+    bool fast = false;
+    int block = 0;
+    int64_t grid = 0;
+};
+QuantPlan plan_int4_quantize(int64_t n, int64_t k, const void* w, const void* wp);
+QuantPlan plan_q8_quantize(int64_t n, int64_t k, const void* w, const void* wq);
+// `rcp`: scale = amax * fl(1/qmax) (torch's form on a GPU) instead of
+// amax / qmax (torch's form on the CPU).
+hipError_t launch_int4_quantize(const QuantPlan& p, const void* w, void* wp,
+                                void* scale, int64_t n, int64_t k, bool rcp,
+                                hipStream_t stream);
+hipError_t launch_q8_quantize(const QuantPlan& p, const void* w, void* wq,
+                              void* scale, int64_t n, int64_t k, bool rcp,
+                              hipStream_t stream);
+
 // Plain streaming read of `bytes` (a multiple of 16) from `buf`: the
 // bandwidth ceiling of one launch reading that many bytes.
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

@@ -1,0 +1,321 @@
+// On-device weight quantizers for the two GEMV operators (gfx950).
+//
+//   INT4, group-wise (cudalab/int4gemv_quantize.py:61-114, quantize_w + pack_q):
+//     per group of 128 consecutive elements of a row
+//       s32 = fp32(amax |W|) / 7
+//       q   = clamp(rint_half_even(fl(W / s32)), -7, 7), q = 0 if s32 == 0
+//       packed byte b of the group = (q[2b] & 15) | (q[2b+1] & 15) << 4
+//       scale = fp16(s32), round to nearest even
+//   INT8, per row (cudalab/qgemv_quantize.py:33-64):
+//       s = fp32(amax |W_row|) / 127, q = clamp(rint(fl(W / s)), -127, 127),
+//       q = 0 if s == 0, scale stored as fp32.
+//
+// The reference writes the scale as `amax / INT4_MAX` (a tensor divided by
+// a Python number), which torch evaluates differently by device: on the CPU
+// as one correctly rounded division, on a GPU as amax * fl(1 / 7) (a CPU
+// scalar divisor becomes a multiplication by its float reciprocal).  The
+// two differ by one fp32 step for about half of all fp16 amax values, which
+// moves q at exact ties.  `rcp` selects the GPU form; otherwise the CPU
+// form.  The division w / s is a tensor-by-tensor division on both devices
+// (correctly rounded).
+//
+// The outputs are bit-identical to those definitions.  Non-finite W is not
+// rejected here: a group (INT4) or row (INT8) holding NaN/Inf gets a
+// non-finite scale, and no finite input can give one (|amax| <= 65504), so a
+// caller checks the scale, not all of W.
+//
+// Fast path.  Row-major W with K % 128 == 0 is a flat sequence of groups,
+// group g being elements [128 g, 128 g + 128) and scale element g.  Sixteen
+// lanes (one DPP row) take one group, 8 fp16 (16 bytes) each; a wave reads
+// 1 KiB of consecutive groups per load.  The amax is a max over fp16 bit
+// patterns with the sign cleared (for non-negative fp16 the bit-pattern
+// order is the value order), reduced across the 16 lanes with DPP row
+// rotations.  The quotient is estimated as t = w * r, r = v_rcp_f32(s)
+// (at most 2 ulp from 1/s assumed, 1 documented), then rounded to an integer
+// by adding 1.5 * 2^23 (RNE to integers for |t| < 2^22, the integer in the
+// low mantissa bits).  |t - fl(w / s)| <= |q_max| * (2^-22 + 2^-24) * (1 + 2^-23)
+// + ulp(q_max) / 2, which is below 2.4e-6 for q_max = 7 and 4.3e-5 for 127.
+// When t is farther than kNear from every half-integer, rint(t) = rint(fl(w/s))
+// (no half-integer lies between them).  A lane with any element closer than
+// that recomputes its 8 elements with the correctly rounded division.
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "cq_internal.h"
+
+namespace cq {
+namespace {
+
+constexpr float kRoundMagic = 12582912.0f;          // 1.5 * 2^23
+constexpr float kNear4 = 0.5f - 0x1p-18f;           // 3.8e-6 from a half-integer
+constexpr float kNear8 = 0.5f - 0x1p-13f;           // 1.2e-4 from a half-integer
+constexpr int kQBlock = 256;
+
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_elementwise_max(__builtin_bit_cast(us2, a),
+                                                        __builtin_bit_cast(us2, b)));
+}
+
+// Largest |fp16| bit pattern of the 8 values in v (sign bits cleared).
+__device__ __forceinline__ uint32_t amax_bits8(uint4 v) {
+    const uint32_t m = 0x7FFF7FFFu;
+    const uint32_t a = pk_max_u16(pk_max_u16(v.x & m, v.y & m),
+                                  pk_max_u16(v.z & m, v.w & m));
+    return max(a & 0xFFFFu, a >> 16);
+}
+
+// Max over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1).  Every lane of
+// the row must be active.
+__device__ __forceinline__ uint32_t row16_max(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, false));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+    v = row16_max(v);
+    v = max(v, (uint32_t)__shfl_xor((int)v, 16));
+    v = max(v, (uint32_t)__shfl_xor((int)v, 32));
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+    return __builtin_bit_cast(unsigned short, (_Float16)f);
+}
+
+// Scale of a group / row from its amax: the CPU form (one correctly rounded
+// division) or the GPU form (product with the float reciprocal of qmax,
+// folded at compile time with round-to-nearest-even).
+template <int QMAX>
+__device__ __forceinline__ float scale_of(float amax, bool rcp) {
+    constexpr float inv = 1.0f / (float)QMAX;
+    return rcp ? amax * inv : amax / (float)QMAX;
+}
+
+// The definition: clamp(rint(fl(w / s)), -qmax, qmax), 0 when s == 0.
+__device__ __forceinline__ int quant_exact(float w, float s, float qmax) {
+    if (s == 0.f) return 0;
+    float q = rintf(w / s);
+    q = fminf(fmaxf(q, -qmax), qmax);
+    return (int)q;
+}
+
+// Reciprocal used by the estimate; 0 for a zero scale, so t = 0 and q = 0.
+__device__ __forceinline__ float quant_rcp(float s) {
+    return s == 0.f ? 0.f : __builtin_amdgcn_rcpf(s);
+}
+
+// Fast estimate for one element: returns the rounded value's low mantissa
+// bits (the integer mod 2^22) and flags a near-tie.
+__device__ __forceinline__ uint32_t quant_fast(float w, float r, float near_lim,
+                                               bool& near) {
+    const float t = w * r;
+    const float m = t + kRoundMagic;
+    const float d = t - (m - kRoundMagic);
+    near |= fabsf(d) > near_lim;
+    return __float_as_uint(m);
+}
+
+__device__ __forceinline__ float half_of(uint4 v, int i) {
+    const uint32_t w = (i < 2) ? v.x : (i < 4) ? v.y : (i < 6) ? v.z : v.w;
+    return h2f((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+}
+
+// 8 fp16 -> 8 nibbles (element i at bits 4i..4i+3).
+__device__ __forceinline__ uint32_t int4_pack8(uint4 v, float s, float r) {
+    bool near = false;
+    uint32_t out = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        out |= (quant_fast(half_of(v, i), r, kNear4, near) & 0xFu) << (4 * i);
+    if (near) {
+        out = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            out |= ((uint32_t)quant_exact(half_of(v, i), s, 7.f) & 0xFu) << (4 * i);
+    }
+    return out;
+}
+
+// 8 fp16 -> 8 int8 (element i in byte i).
+__device__ __forceinline__ uint2 q8_pack8(uint4 v, float s, float r) {
+    bool near = false;
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = quant_fast(half_of(v, i), r, kNear8, near) & 0xFFu;
+    if (near) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b[i] = (uint32_t)quant_exact(half_of(v, i), s, 127.f) & 0xFFu;
+    }
+    return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                      b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+}
+
+// ---------------------------------------------------------------- INT4 ---
+// Fast kernel: 16 lanes per group, kInt4Steps groups per 16-lane row,
+// 16 * kInt4Steps groups per 256-thread workgroup.  Requires w 16-byte and
+// wp 4-byte aligned.
+constexpr int kInt4Steps = 4;
+constexpr int kInt4GroupsPerBlock = (kQBlock / 16) * kInt4Steps;
+
+__global__ __launch_bounds__(kQBlock) void int4_quantize_kernel(
+        const uint4* __restrict__ w, uint32_t* __restrict__ wp,
+        uint16_t* __restrict__ scale, int64_t groups, bool rcp) {
+    const int lane16 = threadIdx.x & 15;
+    const int64_t g0 = (int64_t)blockIdx.x * kInt4GroupsPerBlock + (threadIdx.x >> 4);
+    // Out-of-range slots (the last workgroup) re-read the last group and
+    // store nothing, so every load is one unconditional 16-byte load.
+    uint4 v[kInt4Steps];
+#pragma unroll
+    for (int u = 0; u < kInt4Steps; ++u) {
+        const int64_t g = min(g0 + u * (kQBlock / 16), groups - 1);
+        v[u] = w[g * 16 + lane16];
+    }
+#pragma unroll
+    for (int u = 0; u < kInt4Steps; ++u) {
+        const int64_t g = g0 + u * (kQBlock / 16);
+        const float s = scale_of<7>(h2f(row16_max(amax_bits8(v[u]))), rcp);
+        const uint32_t packed = int4_pack8(v[u], s, quant_rcp(s));
+        if (g < groups) {
+            wp[g * 16 + lane16] = packed;
+            if (lane16 == 0) scale[g] = f2h_bits(s);
+        }
+    }
+}
+
+// Generic kernel (any 2-byte aligned w, any wp): one wave per group, two
+// elements per lane, the definition evaluated directly.
+__global__ __launch_bounds__(kQBlock) void int4_quantize_generic_kernel(
+        const uint16_t* __restrict__ w, uint8_t* __restrict__ wp,
+        uint16_t* __restrict__ scale, int64_t groups, bool rcp) {
+    const int64_t g = (int64_t)blockIdx.x * (kQBlock / 64) + (threadIdx.x >> 6);
+    if (g >= groups) return;                       // uniform over the wave
+    const int lane = threadIdx.x & 63;
+    const uint32_t e0 = w[g * 128 + 2 * lane], e1 = w[g * 128 + 2 * lane + 1];
+    const uint32_t am = wave_max(max(e0 & 0x7FFFu, e1 & 0x7FFFu));
+    const float s = scale_of<7>(h2f(am), rcp);
+    const uint32_t q0 = (uint32_t)quant_exact(h2f(e0), s, 7.f) & 0xFu;
+    const uint32_t q1 = (uint32_t)quant_exact(h2f(e1), s, 7.f) & 0xFu;
+    wp[g * 64 + lane] = (uint8_t)(q0 | (q1 << 4));
+    if (lane == 0) scale[g] = f2h_bits(s);
+}
+
+// ---------------------------------------------------------------- INT8 ---
+// Fast kernel: one 256-thread workgroup per row, kQ8Held 16-byte chunks per
+// thread held in registers between the amax and the quantize pass (rows up
+// to 256 * 8 * kQ8Held elements); longer rows re-read the rest (from L2).
+// Requires k % 8 == 0, w 16-byte and wq 8-byte aligned.
+constexpr int kQ8Held = 8;
+
+__global__ __launch_bounds__(kQBlock) void q8_quantize_kernel(
+        const uint4* __restrict__ w, uint2* __restrict__ wq,
+        float* __restrict__ scale, int64_t chunks, bool rcp) {
+    __shared__ uint32_t red[kQBlock / 64];
+    const int64_t row = blockIdx.x;
+    const uint4* src = w + row * chunks;
+    uint2* dst = wq + row * chunks;
+    uint4 v[kQ8Held];
+    uint32_t am = 0;
+#pragma unroll
+    for (int h = 0; h < kQ8Held; ++h) {
+        const int64_t c = threadIdx.x + (int64_t)h * kQBlock;
+        v[h] = c < chunks ? src[c] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < kQ8Held; ++h) am = max(am, amax_bits8(v[h]));
+    for (int64_t c = threadIdx.x + (int64_t)kQ8Held * kQBlock; c < chunks; c += kQBlock)
+        am = max(am, amax_bits8(src[c]));
+    am = wave_max(am);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    am = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float s = scale_of<127>(h2f(am), rcp);
+    const float r = quant_rcp(s);
+    if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+    for (int h = 0; h < kQ8Held; ++h) {
+        const int64_t c = threadIdx.x + (int64_t)h * kQBlock;
+        if (c < chunks) dst[c] = q8_pack8(v[h], s, r);
+    }
+    for (int64_t c = threadIdx.x + (int64_t)kQ8Held * kQBlock; c < chunks; c += kQBlock)
+        dst[c] = q8_pack8(src[c], s, r);
+}
+
+// Generic kernel (any k, any 2-byte aligned w): one workgroup per row,
+// element by element, the definition evaluated directly.
+__global__ __launch_bounds__(kQBlock) void q8_quantize_generic_kernel(
+        const uint16_t* __restrict__ w, int8_t* __restrict__ wq,
+        float* __restrict__ scale, int64_t k, bool rcp) {
+    __shared__ uint32_t red[kQBlock / 64];
+    const int64_t row = blockIdx.x;
+    const uint16_t* src = w + row * k;
+    uint32_t am = 0;
+    for (int64_t i = threadIdx.x; i < k; i += kQBlock) am = max(am, (uint32_t)(src[i] & 0x7FFFu));
+    am = wave_max(am);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    am = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float s = scale_of<127>(h2f(am), rcp);
+    if (threadIdx.x == 0) scale[row] = s;
+    for (int64_t i = threadIdx.x; i < k; i += kQBlock)
+        wq[row * k + i] = (int8_t)quant_exact(h2f(src[i]), s, 127.f);
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+QuantPlan plan_int4_quantize(int64_t n, int64_t k, const void* w, const void* wp) {
+    QuantPlan p;
+    const int64_t groups = n * (k / 128);
+    p.fast = aligned(w, 16) && aligned(wp, 4);
+    p.block = kQBlock;
+    p.grid = p.fast ? (groups + kInt4GroupsPerBlock - 1) / kInt4GroupsPerBlock
+                    : (groups + kQBlock / 64 - 1) / (kQBlock / 64);
+    return p;
+}
+
+QuantPlan plan_q8_quantize(int64_t n, int64_t k, const void* w, const void* wq) {
+    QuantPlan p;
+    p.fast = k % 8 == 0 && aligned(w, 16) && aligned(wq, 8);
+    p.block = kQBlock;
+    p.grid = n;
+    return p;
+}
+
+hipError_t launch_int4_quantize(const QuantPlan& p, const void* w, void* wp,
+                                void* scale, int64_t n, int64_t k, bool rcp,
+                                hipStream_t stream) {
+    const int64_t groups = n * (k / 128);
+    if (p.fast)
+        int4_quantize_kernel<<<dim3((unsigned)p.grid), dim3(kQBlock), 0, stream>>>(
+            (const uint4*)w, (uint32_t*)wp, (uint16_t*)scale, groups, rcp);
+    else
+        int4_quantize_generic_kernel<<<dim3((unsigned)p.grid), dim3(kQBlock), 0, stream>>>(
+            (const uint16_t*)w, (uint8_t*)wp, (uint16_t*)scale, groups, rcp);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_quantize(const QuantPlan& p, const void* w, void* wq,
+                              void* scale, int64_t n, int64_t k, bool rcp,
+                              hipStream_t stream) {
+    if (p.fast)
+        q8_quantize_kernel<<<dim3((unsigned)p.grid), dim3(kQBlock), 0, stream>>>(
+            (const uint4*)w, (uint2*)wq, (float*)scale, k / 8, rcp);
+    else
+        q8_quantize_generic_kernel<<<dim3((unsigned)p.grid), dim3(kQBlock), 0, stream>>>(
+            (const uint16_t*)w, (int8_t*)wq, (float*)scale, k, rcp);
+    return hipGetLastError();
+}
+
+}  // namespace cq

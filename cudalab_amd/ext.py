@@ -624,3 +624,58 @@ def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
     us = tot.value / n_launches
     return {"bytes": nbytes, "us_per_call": us, "GBps": nbytes / us / 1e3,
             "pool_buffers": n}
+
+
+# ---------------------------------------------------------------- quantizers
+def _quant_launch(fn, what: str, W: torch.Tensor, q: torch.Tensor,
+                  scale: torch.Tensor, rcp: bool) -> None:
+    mode = _capi.CQ_SCALE_RCP if rcp else _capi.CQ_SCALE_DIV
+    dev = W.device
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        st = fn(W.data_ptr(), q.data_ptr(), scale.data_ptr(), W.size(0),
+                W.size(1), mode, stream)
+    if st != _capi.CQ_OK:
+        _fail(f"{what} failed (status {st}): {_capi.last_error()}")
+
+
+def quantize_int4(W: torch.Tensor, rcp: bool = True
+                  ) -> tuple[torch.Tensor, torch.Tensor]:
+    """On-device INT4 quantize + pack (cq_int4_quantize) of a CUDA fp16
+    contiguous W (N, K), N, K >= 1, K % 128 == 0 (the caller checks the
+    metadata).  Returns (W_packed uint8 (N, K/2), scale fp16 (N, K/128)),
+    asynchronous on the current stream.  A group holding NaN/Inf gets a
+    non-finite scale.  `rcp`: scale32 = amax * fl(1/7), as torch computes
+    `amax / 7` for a GPU tensor; otherwise amax / 7 correctly rounded, as
+    torch computes it for a CPU tensor."""
+    N, K = W.shape
+    wp = torch.empty((N, K // 2), dtype=torch.uint8, device=W.device)
+    scale = torch.empty((N, K // 128), dtype=torch.float16, device=W.device)
+    _quant_launch(_capi.load().cq_int4_quantize, "int4 quantize", W, wp, scale,
+                  rcp)
+    return wp, scale
+
+
+def quantize_q8(W: torch.Tensor, rcp: bool = True
+                ) -> tuple[torch.Tensor, torch.Tensor]:
+    """On-device per-row INT8 quantize (cq_q8_quantize) of a CUDA fp16
+    contiguous W (N, K), N, K >= 1.  Returns (W_q int8 (N, K), scale
+    float32 (N,)), asynchronous on the current stream.  A row holding
+    NaN/Inf gets a non-finite scale.  `rcp` as for quantize_int4 (with
+    127)."""
+    N, K = W.shape
+    wq = torch.empty((N, K), dtype=torch.int8, device=W.device)
+    scale = torch.empty((N,), dtype=torch.float32, device=W.device)
+    _quant_launch(_capi.load().cq_q8_quantize, "int8 quantize", W, wq, scale,
+                  rcp)
+    return wq, scale
+
+
+def quantize_vectorized(op: str, W: torch.Tensor, out: torch.Tensor) -> bool:
+    """Whether the quantizer of `op` ("int4gemv" | "qgemv") takes its
+    vectorized kernel for these tensors (same results either way)."""
+    r = _capi.load().cq_quantize_vectorized(_capi.OPS[op], W.data_ptr(),
+                                            out.data_ptr(), W.size(0), W.size(1))
+    if r < 0:
+        _fail(f"quantize_vectorized: {_capi.last_error()}")
+    return bool(r)

@@ -17,7 +17,9 @@ Nibble packing: byte b of a row holds element 2b in bits 0-3 and element
 sign-extends (codes 8..15 are -8..-1).
 
 Quantization and packing run offline, outside every timed region.  The
-functions work on CPU and GPU tensors alike.
+functions work on CPU and GPU tensors alike: `quantize_w` of a CUDA tensor
+runs the on-device HIP quantizer (one launch, bit-identical to the torch
+formulation `quantize_w_torch`, which serves CPU tensors).
 """
 from __future__ import annotations
 
@@ -27,7 +29,7 @@ INT4_MAX = 7
 GROUP_SIZE = 128
 
 
-def _check_w(W: torch.Tensor) -> None:
+def _check_w(W: torch.Tensor, finite: bool = True) -> None:
     if W.dim() != 2:
         raise ValueError(f"expected a 2-D W (N, K), got {W.dim()}-D")
     if W.dtype != torch.float16:
@@ -37,21 +39,68 @@ def _check_w(W: torch.Tensor) -> None:
     if W.size(1) % GROUP_SIZE != 0:
         raise ValueError(f"K must be divisible by {GROUP_SIZE} "
                          f"(group size), got K={W.size(1)}")
-    if not bool(torch.isfinite(W).all()):
-        raise ValueError("the quantizer requires finite W (NaN/Inf found)")
+    if finite and not bool(torch.isfinite(W).all()):
+        raise ValueError(_NONFINITE)
 
 
-def quantize_w(W: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+_NONFINITE = "the quantizer requires finite W (NaN/Inf found)"
+
+
+def _scale32(amax: torch.Tensor, qmax: int, rcp: bool | None) -> torch.Tensor:
+    """amax / qmax in FP32: as written (torch's own per-device rounding) for
+    rcp None, else forced to amax * fl(1/qmax) (True) or a correctly rounded
+    division (False)."""
+    if rcp is None:
+        return amax / qmax
+    if rcp:
+        # fl32(1/qmax), held exactly by a Python float; the product rounds once
+        inv = (torch.ones((), dtype=torch.float32) / qmax).item()
+        return amax * inv
+    # a divisor tensor on amax's own device: a true division everywhere
+    return amax / torch.tensor(float(qmax), dtype=torch.float32, device=amax.device)
+
+
+def quantize_w(W: torch.Tensor, semantics: str | None = None
+               ) -> tuple[torch.Tensor, torch.Tensor]:
     """Symmetric group-wise INT4 quantization of fp16 W (N, K), K % 128 == 0.
 
     Returns (W_packed uint8 (N, K/2), scale fp16 (N, K/128)).
     Raises ValueError for non-2-D, non-fp16, non-contiguous, K % 128 != 0,
-    or non-finite input."""
+    or non-finite input.
+
+    A CUDA W is quantized and packed by the HIP kernel (cq_int4_quantize)
+    in one pass; its non-finite check reads the scale, which is non-finite
+    exactly where a group of W holds NaN/Inf.  An empty W launches nothing
+    and gets the torch formulation's empty results.
+
+    `semantics` picks how `amax / qmax` is rounded, as the reference's
+    torch code does on each device: "cpu" one correctly rounded division,
+    "gpu" amax * fl(1/qmax) (torch applies a CPU-scalar divisor on a GPU as
+    its reciprocal).  The default is W's own device, so the result equals
+    the reference's `quantize_w` on the same tensor."""
+    if semantics not in (None, "cpu", "gpu"):
+        raise ValueError(f"semantics must be None, 'cpu' or 'gpu', got {semantics!r}")
+    if W.is_cuda and W.numel() > 0:
+        _check_w(W, finite=False)
+        from .ext import quantize_int4
+        W_packed, scale = quantize_int4(W, rcp=semantics != "cpu")
+        if not bool(torch.isfinite(scale).all()):
+            raise ValueError(_NONFINITE)
+        return W_packed, scale
+    return quantize_w_torch(W, rcp=None if semantics is None else semantics == "gpu")
+
+
+def quantize_w_torch(W: torch.Tensor, rcp: bool | None = None
+                     ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The quantizer as torch tensor operations (the reference's
+    formulation, cudalab/int4gemv_quantize.py:61-89), on W's device.
+    `rcp` None divides by the Python number as the reference does (torch
+    rounds that per device); True / False force amax * fl(1/7) / amax / 7."""
     _check_w(W)
     N, K = W.shape
     G = K // GROUP_SIZE
     groups = W.float().reshape(N, G, GROUP_SIZE)
-    s32 = groups.abs().amax(dim=2) / INT4_MAX           # (N, G) FP32
+    s32 = _scale32(groups.abs().amax(dim=2), INT4_MAX, rcp)   # (N, G) FP32
     is_zero = s32 == 0
     denom = torch.where(is_zero, torch.ones_like(s32), s32)
     q = torch.round(groups / denom.unsqueeze(2))        # half to even

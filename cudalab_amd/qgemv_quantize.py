@@ -17,21 +17,58 @@ import torch
 INT8_MAX = 127
 
 
-def quantize_w(W: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Symmetric per-row INT8 quantization of fp16 W (N, K).
+_NONFINITE = "the quantizer requires finite W (NaN/Inf found)"
 
-    Returns (W_q int8 (N, K), scale float32 (N,)).  Raises ValueError for
-    non-2-D, non-fp16, non-contiguous or non-finite input."""
+
+def _check_w(W: torch.Tensor, finite: bool = True) -> None:
     if W.dim() != 2:
         raise ValueError(f"expected a 2-D W (N, K), got {W.dim()}-D")
     if W.dtype != torch.float16:
         raise ValueError(f"the quantizer takes fp16 weights only, got {W.dtype}")
     if not W.is_contiguous():
         raise ValueError("the quantizer requires a contiguous W")
-    if not bool(torch.isfinite(W).all()):
-        raise ValueError("the quantizer requires finite W (NaN/Inf found)")
+    if finite and not bool(torch.isfinite(W).all()):
+        raise ValueError(_NONFINITE)
+
+
+def quantize_w(W: torch.Tensor, semantics: str | None = None
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-row INT8 quantization of fp16 W (N, K).
+
+    Returns (W_q int8 (N, K), scale float32 (N,)).  Raises ValueError for
+    non-2-D, non-fp16, non-contiguous or non-finite input.
+
+    A CUDA W is quantized by the HIP kernel (cq_q8_quantize) in one launch;
+    its non-finite check reads the scale, which is non-finite exactly for
+    the rows of W holding NaN/Inf.  An empty W launches nothing and gets
+    the torch formulation's result.
+
+    `semantics` picks how `amax / qmax` is rounded, as the reference's
+    torch code does on each device: "cpu" one correctly rounded division,
+    "gpu" amax * fl(1/qmax) (torch applies a CPU-scalar divisor on a GPU as
+    its reciprocal).  The default is W's own device, so the result equals
+    the reference's `quantize_w` on the same tensor."""
+    if semantics not in (None, "cpu", "gpu"):
+        raise ValueError(f"semantics must be None, 'cpu' or 'gpu', got {semantics!r}")
+    if W.is_cuda and W.numel() > 0:
+        _check_w(W, finite=False)
+        from .ext import quantize_q8
+        W_q, scale = quantize_q8(W, rcp=semantics != "cpu")
+        if not bool(torch.isfinite(scale).all()):
+            raise ValueError(_NONFINITE)
+        return W_q, scale
+    return quantize_w_torch(W, rcp=None if semantics is None else semantics == "gpu")
+
+
+def quantize_w_torch(W: torch.Tensor, rcp: bool | None = None
+                     ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The quantizer as torch tensor operations (the reference's
+    formulation, cudalab/qgemv_quantize.py:33-64), on W's device.  `rcp` as
+    in int4gemv_quantize.quantize_w_torch."""
+    from .int4gemv_quantize import _scale32
+    _check_w(W)
     Wf = W.float()
-    scale = Wf.abs().amax(dim=1) / INT8_MAX              # (N,) FP32
+    scale = _scale32(Wf.abs().amax(dim=1), INT8_MAX, rcp)  # (N,) FP32
     is_zero = scale == 0
     denom = torch.where(is_zero, torch.ones_like(scale), scale)
     q = torch.round(Wf / denom.unsqueeze(1)).clamp(-INT8_MAX, INT8_MAX)

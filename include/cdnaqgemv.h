@@ -73,6 +73,13 @@ extern "C" {
 #define CQ_DTYPE_F16 0
 #define CQ_DTYPE_F32 1
 
+/* quantizer scale forms (cq_int4_quantize, cq_q8_quantize): the reference
+ * computes the scale as `amax / qmax` in torch, which is one correctly
+ * rounded division for a CPU tensor and amax * fl(1 / qmax) for a GPU
+ * tensor (torch applies a CPU-scalar divisor as its reciprocal) */
+#define CQ_SCALE_DIV 0   /* amax / qmax: the reference run on the CPU */
+#define CQ_SCALE_RCP 1   /* amax * fl(1/qmax): the reference run on a GPU */
+
 /* variant list selectors */
 #define CQ_LIST_NORMAL      0
 #define CQ_LIST_ALL         1
@@ -133,6 +140,43 @@ int cq_int4gemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
                         int64_t n_problems, int64_t k, void* stream);
 int cq_qgemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
                      int64_t n_problems, int64_t k, void* stream);
+
+/*
+ * On-device INT4 quantize + pack of fp16 w [n, k] (k % 128 == 0) into
+ * w_packed uint8 [n, k/2] and scale fp16 [n, k/128]: per group of 128,
+ * s = fp32 amax / 7 in the form `scale_mode` names (CQ_SCALE_DIV or
+ * CQ_SCALE_RCP), q = clamp(rint_half_even(w / s), -7, 7) (0 for a zero
+ * group), element 2b in the low nibble of byte b, scale = fp16(s).
+ * Bit-identical to `quantize_w` + `pack_q`
+ * (cudalab/int4gemv_quantize.py:61-114), which the reference runs as torch
+ * ops, on the CPU (CQ_SCALE_DIV) or on a GPU (CQ_SCALE_RCP).  Asynchronous
+ * on `stream`.  NaN/Inf in w is not rejected: the scale of every group
+ * holding one is non-finite, and finite w never gives a non-finite scale,
+ * so a caller checks the scale.
+ */
+int cq_int4_quantize(const void* w, void* w_packed, void* scale, int64_t n,
+                     int64_t k, int scale_mode, void* stream);
+
+/*
+ * On-device INT8 quantize of fp16 w [n, k] (any k >= 1) into w_q int8
+ * [n, k] and scale fp32 [n]: s = fp32 row amax / 127 (form per
+ * `scale_mode`), q = clamp(rint_half_even(w / s), -127, 127), 0 for a zero
+ * row.  Bit-identical to `quantize_w` (cudalab/qgemv_quantize.py:33-64) on
+ * the CPU (CQ_SCALE_DIV) or a GPU (CQ_SCALE_RCP).  NaN/Inf as for
+ * cq_int4_quantize (per row).
+ */
+int cq_q8_quantize(const void* w, void* w_q, void* scale, int64_t n, int64_t k,
+                   int scale_mode, void* stream);
+
+/*
+ * 1 if the quantizer of `op` (CQ_OP_INT4GEMV or CQ_OP_QGEMV) takes its
+ * vectorized kernel for these pointers and sizes (w 16-byte aligned,
+ * output 4-byte (INT4) or 8-byte (INT8) aligned, k % 8 == 0 for INT8),
+ * 0 if it takes the element-wise kernel (same results), -1 for another op.
+ * No reference counterpart (the reference quantizes with torch ops).
+ */
+int cq_quantize_vectorized(int op, const void* w, const void* out, int64_t n,
+                           int64_t k);
 
 /* Result of cq_native_timing; all times are per launch, microseconds. */
 typedef struct cq_timing {

@@ -11,7 +11,9 @@ the reference repository).  How each is pinned (tests/test_oracle_*.py):
                           (tests/test_int4gemv_cpu.py:53-108 of the reference)
   quantize_w4 / _w8       closed-form invariants (scale == fp16(amax/7),
                           q == clamp(rint(W/s32)), zero groups, step bound,
-                          half-even ties) and numpy == C == cudalab_amd
+                          half-even ties) and numpy == C == cudalab_amd;
+                          the `rcp` scale form against a float64 restatement
+                          of fl(amax * fl(1/qmax)) over every fp16 amax
   exact_w4 / exact_w8     exact rational arithmetic (fractions.Fraction) on
                           small inputs, one-hot and all-ones closed forms
   ref_f32_w4 / _w8        sequential FP32 sum replayed in numpy float32
@@ -66,8 +68,8 @@ def lib():
         L.orc_q8_exact.restype = ctypes.c_int
         L.orc_int4_ref_f32.argtypes = [P, P, P, i64, i64, P, P]
         L.orc_q8_ref_f32.argtypes = [P, P, P, i64, i64, P, P]
-        L.orc_int4_quantize.argtypes = [P, i64, i64, P, P]
-        L.orc_q8_quantize.argtypes = [P, i64, i64, P, P]
+        L.orc_int4_quantize.argtypes = [P, i64, i64, P, P, ctypes.c_int]
+        L.orc_q8_quantize.argtypes = [P, i64, i64, P, P, ctypes.c_int]
         L.orc_unpack_bytes.argtypes = [P, i64, P]
         L.orc_int4_gemv_cpu.argtypes = [P, P, P, P, i64, i64, ctypes.c_int, P]
         L.orc_q8_gemv_cpu.argtypes = [P, P, P, P, i64, i64, ctypes.c_int, P]
@@ -131,16 +133,29 @@ def unpack_w_c(wp: np.ndarray) -> np.ndarray:
 
 # ----------------------------------------------------- quantizers (numpy)
 
-def quantize_w4(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Group-wise INT4 (cudalab/int4gemv_quantize.py:61-89): FP32 amax/7,
-    round half to even, clamp +-7, zero groups -> 0; returns (uint8 packed,
-    fp16 scale)."""
+def _scale(amax: np.ndarray, qmax: int, rcp: bool) -> np.ndarray:
+    """amax / qmax in FP32 as torch evaluates `tensor / python_int`: one
+    correctly rounded division for a CPU tensor; for a GPU tensor a product
+    with the FP32 reciprocal fl(1/qmax), rounded once (torch turns a CPU
+    scalar divisor into a multiplication by its reciprocal: PyTorch
+    aten/src/ATen/native/cuda/BinaryDivTrueKernel.cu, div_true_kernel_cuda)."""
+    amax = amax.astype(np.float32)
+    if rcp:
+        inv = np.float32(1) / np.float32(qmax)
+        return (amax * inv).astype(np.float32)
+    return (amax / np.float32(qmax)).astype(np.float32)
+
+
+def quantize_w4(W16: np.ndarray, rcp: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """Group-wise INT4 (cudalab/int4gemv_quantize.py:61-89): FP32 amax/7
+    (see `_scale` for `rcp`), round half to even, clamp +-7, zero groups ->
+    0; returns (uint8 packed, fp16 scale)."""
     W16 = np.asarray(W16, dtype=np.float16)
     N, K = W16.shape
     if K % GROUP_SIZE:
         raise ValueError("K % 128 != 0")
     g = W16.astype(np.float32).reshape(N, K // GROUP_SIZE, GROUP_SIZE)
-    s32 = (np.abs(g).max(axis=2) / np.float32(INT4_MAX)).astype(np.float32)
+    s32 = _scale(np.abs(g).max(axis=2), INT4_MAX, rcp)
     zero = s32 == 0
     denom = np.where(zero, np.float32(1), s32).astype(np.float32)
     q = np.rint((g / denom[:, :, None]).astype(np.float32))
@@ -149,11 +164,11 @@ def quantize_w4(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return pack_q(q.reshape(N, K).astype(np.int64)), s32.astype(np.float16)
 
 
-def quantize_w8(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def quantize_w8(W16: np.ndarray, rcp: bool = False) -> tuple[np.ndarray, np.ndarray]:
     """Per-row INT8 (cudalab/qgemv_quantize.py:33-64): (int8 W_q, fp32
-    scale)."""
+    scale); `rcp` as for quantize_w4."""
     W32 = np.asarray(W16, dtype=np.float16).astype(np.float32)
-    s = (np.abs(W32).max(axis=1) / np.float32(INT8_MAX)).astype(np.float32)
+    s = _scale(np.abs(W32).max(axis=1), INT8_MAX, rcp)
     zero = s == 0
     denom = np.where(zero, np.float32(1), s).astype(np.float32)
     q = np.rint((W32 / denom[:, None]).astype(np.float32))
@@ -162,21 +177,21 @@ def quantize_w8(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q.astype(np.int8), s
 
 
-def quantize_w4_c(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def quantize_w4_c(W16: np.ndarray, rcp: bool = False) -> tuple[np.ndarray, np.ndarray]:
     Wb = _bits16(W16)
     N, K = Wb.shape
     wp = np.empty((N, K // 2), dtype=np.uint8)
     sc = np.empty((N, K // GROUP_SIZE), dtype=np.uint16)
-    lib().orc_int4_quantize(_p(Wb), N, K, _p(wp), _p(sc))
+    lib().orc_int4_quantize(_p(Wb), N, K, _p(wp), _p(sc), int(rcp))
     return wp, sc.view(np.float16)
 
 
-def quantize_w8_c(W16: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def quantize_w8_c(W16: np.ndarray, rcp: bool = False) -> tuple[np.ndarray, np.ndarray]:
     Wb = _bits16(W16)
     N, K = Wb.shape
     wq = np.empty((N, K), dtype=np.int8)
     sc = np.empty((N,), dtype=np.float32)
-    lib().orc_q8_quantize(_p(Wb), N, K, _p(wq), _p(sc))
+    lib().orc_q8_quantize(_p(Wb), N, K, _p(wq), _p(sc), int(rcp))
     return wq, sc
 
 

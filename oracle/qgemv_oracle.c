@@ -12,6 +12,9 @@
  *   orc_int4_quantize   cudalab/int4gemv_quantize.py:61-114 (quantize_w,
  *                       pack_q)
  *   orc_q8_quantize     cudalab/qgemv_quantize.py:33-64
+ *                       (both take `rcp`: the scale amax / qmax as torch
+ *                       evaluates it for a GPU tensor, amax * fl(1/qmax),
+ *                       instead of the CPU's correctly rounded division)
  *   orc_int4_exact      the fp64 "exact" and S_n of the accumulation bound,
  *                       cudalab/int4gemv_correctness.py:175-209, computed
  *                       here in exact integer arithmetic (one rounding)
@@ -225,7 +228,8 @@ void orc_q8_ref_f32(const int8_t* wq, const float* scale, const uint16_t* x,
  * q = 0; pack element 2b low nibble, 2b+1 high nibble; scale stored as
  * fp16(s32). */
 void orc_int4_quantize(const uint16_t* w16, int64_t n, int64_t k, uint8_t* wp,
-                       uint16_t* scale16) {
+                       uint16_t* scale16, int rcp) {
+    const float inv7 = 1.0f / 7.0f;
     const int64_t ng = k / 128;
     for (int64_t r = 0; r < n; ++r) {
         for (int64_t g = 0; g < ng; ++g) {
@@ -235,7 +239,7 @@ void orc_int4_quantize(const uint16_t* w16, int64_t n, int64_t k, uint8_t* wp,
                 const float a = fabsf(h2f(src[i]));
                 if (a > amax) amax = a;
             }
-            const float s32 = amax / 7.0f;
+            const float s32 = rcp ? amax * inv7 : amax / 7.0f;
             uint8_t* dst = wp + r * (k / 2) + g * 64;
             for (int i = 0; i < 64; ++i) {
                 int q[2];
@@ -254,14 +258,15 @@ void orc_int4_quantize(const uint16_t* w16, int64_t n, int64_t k, uint8_t* wp,
 }
 
 void orc_q8_quantize(const uint16_t* w16, int64_t n, int64_t k, int8_t* wq,
-                     float* scale) {
+                     float* scale, int rcp) {
+    const float inv127 = 1.0f / 127.0f;
     for (int64_t r = 0; r < n; ++r) {
         float amax = 0.f;
         for (int64_t i = 0; i < k; ++i) {
             const float a = fabsf(h2f(w16[r * k + i]));
             if (a > amax) amax = a;
         }
-        const float s = amax / 127.0f;
+        const float s = rcp ? amax * inv127 : amax / 127.0f;
         for (int64_t i = 0; i < k; ++i) {
             if (s == 0.f) { wq[r * k + i] = 0; continue; }
             float v = nearbyintf(h2f(w16[r * k + i]) / s);
