@@ -90,6 +90,7 @@ struct QuantPlan {
     bool fast = false;
     int block = 0;
     int64_t grid = 0;
+    int held = 0;   // INT8 fast kernel: 16-byte chunks per thread in registers
 };
 QuantPlan plan_int4_quantize(int64_t n, int64_t k, const void* w, const void* wp);
 QuantPlan plan_q8_quantize(int64_t n, int64_t k, const void* w, const void* wq);

@@ -18,6 +18,7 @@ Reads rocprofv3's CSV output (`-f csv`: *_kernel_trace.csv,
 
 Usage:
   python -m cudalab_amd.evaluator.rocprof_summary trace DIR [--match S]
+      [--top N] [--by-grid]
   python -m cudalab_amd.evaluator.rocprof_summary counters DIR [DIR ...]
       --match S [--match S ...]
   python -m cudalab_amd.evaluator.rocprof_summary traffic --fetch DIR
@@ -57,16 +58,25 @@ def _dbs(d: Path) -> list[Path]:
     return sorted(d.rglob("*.db"))
 
 
-def dispatch_times(d: Path) -> dict[str, list[tuple[int, int]]]:
-    """kernel name -> [(start_ns, end_ns)] in start order."""
+def dispatch_times(d: Path, by_grid: bool = False) -> dict[str, list[tuple[int, int]]]:
+    """kernel name -> [(start_ns, end_ns)] in start order.  With `by_grid`
+    the key also carries the dispatch's grid size (CSV traces), so one
+    kernel launched at several shapes is reported per shape."""
     by: dict[str, list[tuple[int, int]]] = {}
     tables = _csv_rows(d, "kernel_trace.csv")
     for header, rows in tables:
         ni = _col(header, "Kernel_Name", "Name")
         si = _col(header, "Start_Timestamp", "Start")
         ei = _col(header, "End_Timestamp", "End")
+        gi = None
+        if by_grid:
+            try:
+                gi = _col(header, "Grid_Size_X", "Grid_Size", "Grid_SizeX")
+            except KeyError:
+                gi = None
         for r in rows:
-            by.setdefault(r[ni], []).append((int(r[si]), int(r[ei])))
+            key = r[ni] if gi is None else f"{r[ni]} [grid={r[gi]}]"
+            by.setdefault(key, []).append((int(r[si]), int(r[ei])))
     if not tables:
         for db in _dbs(d):
             con = sqlite3.connect(db)
@@ -145,8 +155,9 @@ def _stats_us(ns: list[float]) -> dict:
             "max": s[-1] / 1e3}
 
 
-def report_trace(d: Path, match: str | None, top: int = 8) -> str:
-    by = dispatch_times(d)
+def report_trace(d: Path, match: str | None, top: int = 8,
+                 by_grid: bool = False) -> str:
+    by = dispatch_times(d, by_grid)
     rows = []
     for name, v in by.items():
         st = _stats_us([e - s for s, e in v])
@@ -159,6 +170,9 @@ def report_trace(d: Path, match: str | None, top: int = 8) -> str:
              f"{'min':>8} {'max':>9} {'gap_med':>8}"]
     chosen = [r for r in rows if match and match in r[0]]
     for name, st in (chosen + [r for r in rows if r not in chosen])[:top]:
+        if "[grid=" in name and len(name) > 72:      # keep the grid visible
+            head, grid = name.rsplit(" [grid=", 1)
+            name = head[:72 - len(grid) - 8] + " [grid=" + grid
         lines.append(f"{name[:72]:<72} {st['n']:>6} {st['mean']:>9.3f} "
                      f"{st['median']:>9.3f} {st['min']:>8.3f} {st['max']:>9.3f} "
                      f"{st['gap_median']:>8.3f}")
@@ -229,6 +243,8 @@ def main(argv=None) -> int:
     t.add_argument("dir", type=Path)
     t.add_argument("--match", default=None)
     t.add_argument("--top", type=int, default=8)
+    t.add_argument("--by-grid", action="store_true",
+                   help="one line per (kernel, grid size)")
     c = sub.add_parser("counters")
     c.add_argument("dirs", type=Path, nargs="+")
     c.add_argument("--match", action="append", required=True)
@@ -243,7 +259,7 @@ def main(argv=None) -> int:
     f.add_argument("--json-out", type=Path, default=None)
     a = ap.parse_args(argv)
     if a.cmd == "trace":
-        print(report_trace(a.dir, a.match, a.top))
+        print(report_trace(a.dir, a.match, a.top, a.by_grid))
         return 0
     if a.cmd == "counters":
         print(report_counters(a.dirs, a.match))

@@ -24,10 +24,13 @@ MODES = ("normal", "zeros", "tiny", "large", "mixed_sign")
 INT4_SHAPES = [(1, 128), (3, 128), (16, 256), (8, 128), (1, 4096), (33, 1024),
                (1024, 4096), (4096, 1024), (4096, 4096), (4099, 4096),
                (11008, 4096), (4096, 11008)]
-# (3, 20000): longer than the 16384 elements a workgroup holds in registers
-# (the rest is re-read); (16, 13), (8, 7), (4096, 1): k % 8 != 0, the
-# element-wise kernel.
+# The vectorized INT8 kernel holds 1, 2, 3, 4, 6 or 8 chunks of 8 per
+# thread: (33, 1000), (1, 4096), (7, 6144), (9, 8192), (4, 12288),
+# (4096, 11008) cover each; (3, 20000), (2, 32768), (5, 16392) are longer
+# than the 16384 elements a workgroup holds (the rest is re-read);
+# (16, 13), (8, 7), (4096, 1): k % 8 != 0, the element-wise kernel.
 Q8_SHAPES = [(1, 1), (1, 4096), (4096, 1), (16, 13), (8, 7), (33, 1000),
+             (7, 6144), (9, 8192), (4, 12288),
              (1024, 4096), (4096, 4096), (11008, 4096), (4096, 11008),
              (3, 20000), (2, 32768), (5, 16392)]
 
