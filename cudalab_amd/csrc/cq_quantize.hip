@@ -30,14 +30,24 @@
 // 1 KiB of consecutive groups per load.  The amax is a max over fp16 bit
 // patterns with the sign cleared (for non-negative fp16 the bit-pattern
 // order is the value order), reduced across the 16 lanes with DPP row
-// rotations.  The quotient is estimated as t = w * r, r = v_rcp_f32(s)
-// (at most 2 ulp from 1/s assumed, 1 documented), then rounded to an integer
-// by adding 1.5 * 2^23 (RNE to integers for |t| < 2^22, the integer in the
-// low mantissa bits).  |t - fl(w / s)| <= |q_max| * (2^-22 + 2^-24) * (1 + 2^-23)
-// + ulp(q_max) / 2, which is below 2.4e-6 for q_max = 7 and 4.3e-5 for 127.
-// When t is farther than kNear from every half-integer, rint(t) = rint(fl(w/s))
-// (no half-integer lies between them).  A lane with any element closer than
-// that recomputes its 8 elements with the correctly rounded division.
+// rotations.
+//
+// Quotient.  With r = v_rcp_f32(s) (at most 2 ulp from 1/s assumed, 1
+// documented) the exact product p = w * r satisfies
+// |p - w/s| <= |q_max| * 2^-22, and the correctly rounded quotient
+// F = fl(w/s) satisfies |F - w/s| <= ulp(q_max) / 2; together below 1.9e-6
+// for q_max = 7 and 3.5e-5 for 127.  m = fma(w, r, 1.5 * 2^23) rounds p once
+// to an integer (RNE; the integer k sits in the low mantissa bits of m), and
+// d = fma(w, r, -k) is p - k rounded once.  When |d| <= 1/2 - kNear, p is
+// farther than kNear - 2^-26 from every half-integer, so no half-integer
+// lies between p and F and rint(F) = k.  A lane with any element closer
+// than that recomputes its 8 elements with the correctly rounded division.
+//
+// Packing.  bits(m) = bits(1.5 * 2^23) + k exactly (|k| < 2^22), so packed
+// bytes come from integer sums of the bit patterns with the offset removed
+// by one constant per word: INT4 bytes (k_lo + 8) + 16 (k_hi + 8) and INT8
+// bytes k + 128 lie in [1, 255] (no carries between bytes), then an XOR of
+// 0x88 / 0x80 per byte turns offset binary into two's complement.
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -48,6 +58,11 @@ namespace cq {
 namespace {
 
 constexpr float kRoundMagic = 12582912.0f;          // 1.5 * 2^23
+constexpr uint32_t kMagicBits = 0x4B400000u;         // bits of kRoundMagic
+// word = sum_j p_j << 8j + kPack4Add with p_j = bits(m_lo) + 16 bits(m_hi)
+constexpr uint32_t kPack4Add = (136u - 17u * kMagicBits) * 0x01010101u;
+// word = sum_j bits(m_j) << 8j + kPack8Add
+constexpr uint32_t kPack8Add = (128u - kMagicBits) * 0x01010101u;
 constexpr float kNear4 = 0.5f - 0x1p-18f;           // 3.8e-6 from a half-integer
 constexpr float kNear8 = 0.5f - 0x1p-13f;           // 1.2e-4 from a half-integer
 constexpr int kQBlock = 256;
@@ -87,11 +102,15 @@ __device__ __forceinline__ uint32_t amax_bits8(uint4 v) {
 
 // Max over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1).  Every lane of
 // the row must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
 __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, false));
+    v = max(v, dpp_u32<0x128>(v));
+    v = max(v, dpp_u32<0x124>(v));
+    v = max(v, dpp_u32<0x122>(v));
+    v = max(v, dpp_u32<0x121>(v));
     return v;
 }
 
@@ -132,15 +151,33 @@ __device__ __forceinline__ float quant_rcp(float s) {
     return s == 0.f ? 0.f : __builtin_amdgcn_rcpf(s);
 }
 
-// Fast estimate for one element: returns the rounded value's low mantissa
-// bits (the integer mod 2^22) and flags a near-tie.
+// Fast estimate for one element: bits(m) = kMagicBits + RNE(w * r), and a
+// near-tie flag.
 __device__ __forceinline__ uint32_t quant_fast(float w, float r, float near_lim,
                                                bool& near) {
-    const float t = w * r;
-    const float m = t + kRoundMagic;
-    const float d = t - (m - kRoundMagic);
+    const float m = __builtin_fmaf(w, r, kRoundMagic);
+    const float d = __builtin_fmaf(w, r, -(m - kRoundMagic));
     near |= fabsf(d) > near_lim;
     return __float_as_uint(m);
+}
+
+// The same bit form from an exact integer q.
+__device__ __forceinline__ uint32_t magic_bits(int q) {
+    return kMagicBits + (uint32_t)q;
+}
+
+// 8 magic-bit values (elements 0..7) -> 8 nibbles, element i at bits 4i.
+__device__ __forceinline__ uint32_t pack_nibbles(const uint32_t (&b)[8]) {
+    uint32_t acc = kPack4Add;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += (b[2 * j] + (b[2 * j + 1] << 4)) << (8 * j);
+    return acc ^ 0x88888888u;
+}
+
+// 4 magic-bit values -> 4 int8 bytes, element i in byte i.
+__device__ __forceinline__ uint32_t pack_bytes(uint32_t b0, uint32_t b1, uint32_t b2,
+                                               uint32_t b3) {
+    return (b0 + (b1 << 8) + (b2 << 16) + (b3 << 24) + kPack8Add) ^ 0x80808080u;
 }
 
 __device__ __forceinline__ float half_of(uint4 v, int i) {
@@ -151,17 +188,14 @@ __device__ __forceinline__ float half_of(uint4 v, int i) {
 // 8 fp16 -> 8 nibbles (element i at bits 4i..4i+3).
 __device__ __forceinline__ uint32_t int4_pack8(uint4 v, float s, float r) {
     bool near = false;
-    uint32_t out = 0;
+    uint32_t b[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        out |= (quant_fast(half_of(v, i), r, kNear4, near) & 0xFu) << (4 * i);
+    for (int i = 0; i < 8; ++i) b[i] = quant_fast(half_of(v, i), r, kNear4, near);
     if (near) {
-        out = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            out |= ((uint32_t)quant_exact(half_of(v, i), s, 7.f) & 0xFu) << (4 * i);
+        for (int i = 0; i < 8; ++i) b[i] = magic_bits(quant_exact(half_of(v, i), s, 7.f));
     }
-    return out;
+    return pack_nibbles(b);
 }
 
 // 8 fp16 -> 8 int8 (element i in byte i).
@@ -169,13 +203,12 @@ __device__ __forceinline__ uint2 q8_pack8(uint4 v, float s, float r) {
     bool near = false;
     uint32_t b[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = quant_fast(half_of(v, i), r, kNear8, near) & 0xFFu;
+    for (int i = 0; i < 8; ++i) b[i] = quant_fast(half_of(v, i), r, kNear8, near);
     if (near) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) b[i] = (uint32_t)quant_exact(half_of(v, i), s, 127.f) & 0xFFu;
+        for (int i = 0; i < 8; ++i) b[i] = magic_bits(quant_exact(half_of(v, i), s, 127.f));
     }
-    return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
-                      b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+    return make_uint2(pack_bytes(b[0], b[1], b[2], b[3]), pack_bytes(b[4], b[5], b[6], b[7]));
 }
 
 // ---------------------------------------------------------------- INT4 ---

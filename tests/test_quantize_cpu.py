@@ -5,15 +5,18 @@ The scale has two forms, as the reference's `amax / qmax` (a tensor
 divided by a Python number) is rounded by torch: one correctly rounded
 division on the CPU, amax * fl(1/qmax) on a GPU.  Both are checked.
 
-The HIP kernels estimate q = rint(fl(w / s)) as rint(fl(w * r)) with
-r = v_rcp_f32(s) and recompute with the correctly rounded division only
-for lanes where fl(w * r) is within 2^-18 (INT4) or 2^-13 (INT8) of a
-half-integer.  `_emulate` restates that arithmetic in numpy float32 with r
-moved up to two float32 steps from the correctly rounded 1/s (v_rcp_f32 is
-specified to 1 ulp), and the tests check it against the oracle's
-quantizers (the reference's formula, cudalab/int4gemv_quantize.py:61-114,
-cudalab/qgemv_quantize.py:33-64) on random and crafted inputs, ties
-included.  Dropping the recompute (a planted mistake) must fail."""
+The HIP kernels estimate q = rint(fl(w / s)) as the round-half-even
+integer k of the exact product w * r (one fma), r = v_rcp_f32(s), and
+recompute with the correctly rounded division only for 8-element chunks
+where w * r - k (one more fma) is within 2^-18 (INT4) or 2^-13 (INT8) of
++-1/2; they pack through 32-bit sums of the float bit patterns.
+`_emulate_q` and the `_pack_*` helpers restate that arithmetic in numpy
+with r moved up to two float32 steps from the correctly rounded 1/s
+(v_rcp_f32 is specified to 1 ulp), and the tests check it against the
+oracle's quantizers (the reference's formula,
+cudalab/int4gemv_quantize.py:61-114, cudalab/qgemv_quantize.py:33-64) on
+random and crafted inputs, ties included.  Dropping the recompute (a
+planted mistake) must fail."""
 from __future__ import annotations
 
 from fractions import Fraction
@@ -26,7 +29,9 @@ from oracle import oracle as orc
 
 import quant_cases as qc
 
-MAGIC = np.float32(1.5 * 2 ** 23)
+MAGIC_BITS = np.uint32(0x4B400000)          # bits of 1.5 * 2^23
+PACK4_ADD = np.uint32(((136 - 17 * 0x4B400000) * 0x01010101) % 2 ** 32)
+PACK8_ADD = np.uint32(((128 - 0x4B400000) * 0x01010101) % 2 ** 32)
 NEAR = {7: np.float32(0.5 - 2.0 ** -18), 127: np.float32(0.5 - 2.0 ** -13)}
 
 
@@ -38,11 +43,15 @@ def _step(r: np.ndarray, n: int) -> np.ndarray:
     return out
 
 
-def _emulate(W16: np.ndarray, qmax: int, group: int, rcp_steps: int,
-             recompute: bool = True, rcp_scale: bool = False
-             ) -> tuple[np.ndarray, np.ndarray, int]:
-    """The kernels' arithmetic: returns (q int32 (N, K), s float32 per
-    group, number of 8-element chunks that took the recompute)."""
+def _emulate_q(W16: np.ndarray, qmax: int, group: int, rcp_steps: int,
+               recompute: bool = True, rcp_scale: bool = False):
+    """The kernels' arithmetic: returns (q int64 (N, K), s float32 per
+    group, number of 8-element chunks that took the recompute).
+
+    m = fma(w, r, 1.5 * 2^23) rounds the exact product w * r once: in
+    float64 the product of an fp16 and an fp32 is exact, and rint of it is
+    the round-half-even integer k.  d = fma(w, r, -k) is w * r - k (exact in
+    float64) rounded once to float32."""
     N, K = W16.shape
     w = W16.astype(np.float32).reshape(N, K // group, group)
     amax = np.abs(w).max(axis=2)
@@ -53,10 +62,10 @@ def _emulate(W16: np.ndarray, qmax: int, group: int, rcp_steps: int,
     with np.errstate(divide="ignore"):
         r = np.where(s == 0, np.float32(0), np.float32(1) / s).astype(np.float32)
     r = np.where(s == 0, np.float32(0), _step(r, rcp_steps)).astype(np.float32)
-    t = (w * r[:, :, None]).astype(np.float32)
-    m = (t + MAGIC).astype(np.float32)
-    d = (t - (m - MAGIC).astype(np.float32)).astype(np.float32)
-    q = (m.view(np.uint32).astype(np.int64) - MAGIC.view(np.uint32).astype(np.int64))
+    p = w.astype(np.float64) * r.astype(np.float64)[:, :, None]
+    k = np.rint(p)
+    d = (p - k).astype(np.float32)
+    q = k.astype(np.int64)
     near = (np.abs(d) > NEAR[qmax]).reshape(N, K // 8, 8).any(axis=2)
     if recompute:
         with np.errstate(divide="ignore", invalid="ignore"):
@@ -68,18 +77,60 @@ def _emulate(W16: np.ndarray, qmax: int, group: int, rcp_steps: int,
         ex8 = exact.reshape(N, K // 8, 8).astype(np.int64)
         qc8[near] = ex8[near]
         q = qc8.reshape(N, K // group, group)
-    return q.reshape(N, K).astype(np.int32), s, int(near.sum())
+    return q.reshape(N, K), s, int(near.sum())
+
+
+def _bits(q: np.ndarray) -> np.ndarray:
+    """bits(m) = bits(1.5 * 2^23) + q, as the kernels hold it."""
+    return (MAGIC_BITS.astype(np.int64) + q).astype(np.uint32)
+
+
+def _pack_nibbles(q: np.ndarray) -> np.ndarray:
+    """The kernels' INT4 packing: (N, K) ints in [-7, 7] -> uint8 (N, K/2),
+    through 32-bit sums of the magic bit patterns."""
+    N, K = q.shape
+    b = _bits(q).reshape(N, K // 8, 8)
+    acc = np.full((N, K // 8), PACK4_ADD, dtype=np.uint32)
+    for j in range(4):
+        pj = (b[:, :, 2 * j] + (b[:, :, 2 * j + 1] << np.uint32(4))).astype(np.uint32)
+        acc = (acc + (pj << np.uint32(8 * j))).astype(np.uint32)
+    acc ^= np.uint32(0x88888888)
+    return acc.view(np.uint8).reshape(N, K // 2)
+
+
+def _pack_bytes(q: np.ndarray) -> np.ndarray:
+    """The kernels' INT8 packing: (N, K) ints in [-127, 127], K % 4 == 0 ->
+    int8 (N, K)."""
+    N, K = q.shape
+    b = _bits(q).reshape(N, K // 4, 4)
+    acc = (b[:, :, 0] + (b[:, :, 1] << np.uint32(8)) + (b[:, :, 2] << np.uint32(16))
+           + (b[:, :, 3] << np.uint32(24)) + PACK8_ADD).astype(np.uint32)
+    acc ^= np.uint32(0x80808080)
+    return acc.view(np.int8).reshape(N, K)
 
 
 def _emulate_w4(W16, rcp_steps, recompute=True, rcp_scale=False):
-    q, s, n_near = _emulate(W16, 7, 128, rcp_steps, recompute, rcp_scale)
-    return orc.pack_q(q.astype(np.int64)), s.astype(np.float16), n_near
+    q, s, n_near = _emulate_q(W16, 7, 128, rcp_steps, recompute, rcp_scale)
+    return _pack_nibbles(np.clip(q, -8, 7)), s.astype(np.float16), n_near
 
 
 def _emulate_w8(W16, rcp_steps, recompute=True, rcp_scale=False):
     N, K = W16.shape
-    q, s, n_near = _emulate(W16, 127, K, rcp_steps, recompute, rcp_scale)
-    return q.astype(np.int8), s.reshape(N), n_near
+    q, s, n_near = _emulate_q(W16, 127, K, rcp_steps, recompute, rcp_scale)
+    return _pack_bytes(q), s.reshape(N), n_near
+
+
+def test_packing_identities_exhaustive():
+    """The bit-pattern packing equals the nibble/byte contract for every
+    value pair (INT4) and value (INT8) the quantizers produce."""
+    ks = np.arange(-7, 8)
+    lo, hi = np.meshgrid(ks, ks, indexing="ij")
+    q = np.stack([lo.ravel(), hi.ravel()], axis=1).reshape(1, -1)
+    q = np.concatenate([q, np.zeros((1, (-q.shape[1]) % 8), dtype=q.dtype)], axis=1)
+    assert np.array_equal(_pack_nibbles(q), orc.pack_q(q))
+    q8 = np.arange(-127, 129).reshape(1, -1)
+    q8[0, -1] = 0
+    assert np.array_equal(_pack_bytes(q8), q8.astype(np.int8))
 
 
 @pytest.mark.parametrize("rcp_scale", [False, True], ids=["div", "rcp"])
