@@ -27,6 +27,9 @@
  *     y  same dtype [n]
  *     y[n] = sum_k w[n,k] * x[k] in FP32, cast once to the dtype.
  *
+ * Plus the on-device quantizers that produce the first two operators'
+ * weights from fp16 W (cq_int4_quantize, cq_q8_quantize).
+ *
  * All pointers are device pointers on the current HIP device; `stream` is a
  * hipStream_t (NULL = the null stream).  Calls are asynchronous: a kernel is
  * enqueued and the call returns.  The library never allocates device memory
