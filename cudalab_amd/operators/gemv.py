@@ -162,7 +162,7 @@ class GemvOperator(Operator):
             return BenchPool(xs=[s[1] for s in sets], outs=[s[2] for s in sets],
                              pool_size=n, working_set_bytes=n * set_bytes,
                              element_size=es, mode=mode, launch=launch,
-                             sets=sets, shared_bytes=0,
+                             sets=sets, op="gemv", shared_bytes=0,
                              pool_extra={"hbm_cold": True, "distinct_sets": n,
                                          "set_bytes": set_bytes,
                                          "pool_bytes": n * set_bytes})
@@ -178,7 +178,8 @@ class GemvOperator(Operator):
         return BenchPool(xs=xs, outs=outs, pool_size=n,
                          working_set_bytes=n * es * (K + N), element_size=es,
                          mode=mode, launch=launch, shared=shared,
-                         shared_bytes=N * K * es,
+                         sets=[(W, xs[i], outs[i]) for i in range(n)],
+                         op="gemv", shared_bytes=N * K * es,
                          pool_extra={"hbm_cold": False, "weights_resident": True,
                                      "W_bytes": N * K * es})
 

@@ -120,7 +120,7 @@ class Int4gemvOperator(Operator):
             return BenchPool(xs=xs, outs=outs, pool_size=n,
                              working_set_bytes=n * set_bytes, element_size=2,
                              mode=mode, launch=launch, sets=sets,
-                             shared_bytes=0,
+                             op="int4gemv", shared_bytes=0,
                              pool_extra={"hbm_cold": True,
                                          "distinct_sets": n,
                                          "set_bytes": set_bytes,
@@ -138,7 +138,8 @@ class Int4gemvOperator(Operator):
         return BenchPool(xs=xs, outs=outs, pool_size=n,
                          working_set_bytes=n * 2 * (K + N), element_size=2,
                          mode=mode, launch=launch, shared=shared,
-                         shared_bytes=wp_bytes + scale_bytes,
+                         sets=[(W_packed, scale, xs[i], outs[i]) for i in range(n)],
+                         op="int4gemv", shared_bytes=wp_bytes + scale_bytes,
                          pool_extra={"hbm_cold": False,
                                      "weights_resident": True,
                                      "W_packed_bytes": wp_bytes,

@@ -100,7 +100,7 @@ class QgemvOperator(Operator):
 
             return BenchPool(xs=xs, outs=outs, pool_size=n,
                              working_set_bytes=n * set_bytes, element_size=2,
-                             mode=mode, launch=launch, sets=sets,
+                             mode=mode, launch=launch, sets=sets, op="qgemv",
                              pool_extra={"hbm_cold": True, "distinct_sets": n,
                                          "set_bytes": set_bytes,
                                          "pool_bytes": n * set_bytes})
@@ -117,7 +117,8 @@ class QgemvOperator(Operator):
         return BenchPool(xs=xs, outs=outs, pool_size=n,
                          working_set_bytes=n * 2 * (K + N), element_size=2,
                          mode=mode, launch=launch, shared=shared,
-                         shared_bytes=N * K + 4 * N,
+                         sets=[(W_q, scale, xs[i], outs[i]) for i in range(n)],
+                         op="qgemv", shared_bytes=N * K + 4 * N,
                          pool_extra={"hbm_cold": False,
                                      "weights_resident": True})
 

@@ -1,0 +1,71 @@
+"""GPU tests of the A/B engine (evaluator.bench: measure_block, bench_pair,
+bench_matrix) on the real INT4 path: records are complete, the round
+structure holds, and the fixed decision rules apply to what was measured.
+Short settings (5 rounds, 60 samples of 8 launches) keep each test to
+seconds; the verdicts themselves are not asserted (they depend on the
+hardware), only that they are well formed."""
+from __future__ import annotations
+
+import pytest
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+FAST = dict(rounds=5, warmup=16, iters=60, batch=8)
+
+
+@pytest.fixture(scope="module")
+def op4(ext4):
+    from cudalab_amd.operators import get
+    return get("int4gemv")
+
+
+def test_measure_block_both_calibers(op4, ext4):
+    import torch
+    from cudalab_amd.evaluator.bench import measure_block
+    for mode in ("streaming", "hot"):
+        pool = op4.make_bench_pool(1024, 4096, torch.float16, mode)
+        for caliber in ("native", "api"):
+            announce(f"measure_block {mode} {caliber}")
+            b = measure_block(pool, ext4, "int4gemv_cdna4", warmup=16, iters=60,
+                              batch=8, warmup_ms=50.0, caliber=caliber)
+            assert b["n_raw"] == 60 and b["caliber"] == caliber
+            assert b["n_accepted"] + b["n_rejected_fast"] + b["n_rejected_slow"] == 60
+            assert 0 < b["min_us"] <= b["raw_median_us"]
+            assert b["median_us"] > 0
+        del pool
+
+
+def test_bench_pair_record(op4, ext4):
+    from cudalab_amd.evaluator.ab import decide_pair
+    from cudalab_amd.evaluator.bench import bench_pair
+    from cudalab_amd.evaluator import decision as D
+    announce("bench_pair int4gemv_wave_r2 -> int4gemv_cdna4 1024x4096 streaming")
+    rec = bench_pair(op4, ext4, "int4gemv_wave_r2", "int4gemv_cdna4", 1024, 4096,
+                     mode="streaming", **FAST)
+    assert rec["n_rounds"] == 5 and len(rec["rounds"]) == 5
+    assert [r["order"][0] for r in rec["rounds"]] == \
+        ["int4gemv_wave_r2", "int4gemv_cdna4"] * 2 + ["int4gemv_wave_r2"]
+    assert len(rec["speedups"]) == rec["valid_rounds"]
+    assert all(s > 0 for s in rec["speedups"])
+    assert rec["pool"]["working_set_gt_llc"] and rec["pool"]["pool_extra"]["hbm_cold"]
+    v = decide_pair(rec, True)
+    assert v["policy_decision"] in (D.KEEP, D.REJECT, D.NEUTRAL, D.UNSTABLE)
+    assert v["statistical_relation"] in (D.FASTER, D.SLOWER, D.UNRESOLVED)
+    assert rec["gpu_state_before"] is not None and rec["gpu_state_after"] is not None
+
+
+def test_bench_matrix_cell(op4, ext4):
+    import torch
+    from cudalab_amd.evaluator.bench import analyze_shape_winners, bench_matrix
+    variants = ["int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_wave_r2"]
+    announce("bench_matrix int4gemv 1024x4096 hot")
+    rec = bench_matrix(op4, ext4, variants, 1024, 4096, dtype=torch.float16,
+                       mode="hot", **FAST)
+    assert [r["order"][0] for r in rec["rounds"]] == variants + variants[:2]
+    [cell] = analyze_shape_winners([rec])
+    assert cell["winner"] in variants and cell["runner_up"] in variants
+    assert set(rec["per_variant"]) == set(variants)
+    with pytest.raises(ValueError, match="unknown variant"):
+        bench_matrix(op4, ext4, ["int4gemv_cdna4", "no_such"], 64, 128, **FAST)
