@@ -936,12 +936,17 @@ int default_rows_int4(int64_t n, int slots, int rmax) {
 }
 
 // Workgroup size of the LDS kernels.  512 threads halve the number of
-// workgroups that stage x; measured on MI355X this pays for INT4 with two
-// rows per lane as long as the grid still has a workgroup for every CU
-// (256), and nowhere else at the bench shapes.
+// workgroups that stage x.  Measured on MI355X (same launch path, HBM-cold
+// pools) this pays as long as the grid still has a workgroup for every CU
+// (256) and x is large next to each workgroup's weights: INT4 with two rows
+// per lane (4096^2: 3.82 -> 3.79 us) or with 3+ chunks per lane (4096x11008:
+// 7.44 -> 6.93 us), INT8 with 8+ chunks per lane (4096x11008: 10.48 ->
+// 9.88 us).  INT8 at K = 4096 was 1-3% slower with 512.
 constexpr int64_t kCus = 256;
-int lds_threads(bool int4, int r, int64_t waves) {
-    if (int4 && r == 2 && (waves + 7) / 8 >= kCus) return 512;
+int lds_threads(bool int4, int r, int j, int64_t waves) {
+    const bool fills = (waves + 7) / 8 >= kCus;
+    if (int4 && (r == 2 || j >= 3) && fills) return 512;
+    if (!int4 && j >= 8 && fills) return 512;
     return kBlock;
 }
 
@@ -951,7 +956,7 @@ void finish_wave_plan(Plan& p, int64_t n, bool int4) {
     const int64_t waves = (n + rows_per_wave - 1) / rows_per_wave;
     // the LDS kernels stage x with every thread of a full block
     const int64_t block_waves =
-        p.kind == kLds ? lds_threads(int4, p.r, waves) / 64
+        p.kind == kLds ? lds_threads(int4, p.r, p.j, waves) / 64
                        : std::min<int64_t>(kBlock / 64, waves);
     p.block = static_cast<int>(block_waves * 64);
     p.grid = (waves + block_waves - 1) / block_waves;
@@ -1052,9 +1057,9 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                       static_cast<const float*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    // INT8 plans always use kBlock threads for the LDS kernels
     const Q8Fn fn = p.kind == kWave ? instance<Q8Wave>(p.cw, p.j, p.r)
-                                    : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);
+                    : p.block == 512 ? instance<Q8Lds<512>>(p.cw, p.j, p.r)
+                                     : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 32) : 0;
     return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
@@ -1169,13 +1174,15 @@ hipError_t launch_int4_group(const Plan& p, const GroupProblem* probs,
 
 hipError_t launch_q8_group(const Plan& p, const GroupProblem* probs,
                            int count, int64_t k, hipStream_t stream) {
-    if (p.kind != kLds || count < 1 || count > kMaxGroup || p.block != kBlock)
+    if (p.kind != kLds || count < 1 || count > kMaxGroup)
         return hipErrorInvalidConfiguration;
     GroupArgs g;
     int64_t grid = 0;
     if (!fill_group(p, probs, count, g, grid)) return hipErrorInvalidConfiguration;
-    return launch_group(instance<Q8LdsGroup<kBlock>>(p.cw, p.j, p.r), p, g, grid,
-                        static_cast<uint32_t>(2 * k + 32),
+    const Q8GroupFn fn = p.block == 512
+                             ? instance<Q8LdsGroup<512>>(p.cw, p.j, p.r)
+                             : instance<Q8LdsGroup<kBlock>>(p.cw, p.j, p.r);
+    return launch_group(fn, p, g, grid, static_cast<uint32_t>(2 * k + 32),
                         static_cast<int>(k / 16), stream);
 }
 
@@ -1206,8 +1213,11 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
     p.r = 1;
     const int64_t waves = (n + (64 / p.cw) - 1) / (64 / p.cw);
-    p.block = kBlock;
-    p.grid = (waves + kBlock / 64 - 1) / (kBlock / 64);
+    // 512-thread workgroups halve the x stagings; measured 16% faster at
+    // fp16 4096^2 and 3-4% at 4096x11008 / 11008x4096, when the grid still
+    // covers every CU
+    p.block = (waves + 7) / 8 >= kCus ? 512 : kBlock;
+    p.grid = (waves + p.block / 64 - 1) / (p.block / 64);
     return p;
 }
 
@@ -1215,11 +1225,18 @@ namespace {
 template <typename S>
 using GemvFn = void (*)(const uint4*, const uint4*, S*, int, int);
 
+template <typename S, int NT>
+GemvFn<S> gemv_instance_nt(int cw) {
+    if (cw == 16) return &gemv_lds_kernel<S, 16, NT>;
+    if (cw == 32) return &gemv_lds_kernel<S, 32, NT>;
+    if (cw == 64) return &gemv_lds_kernel<S, 64, NT>;
+    return nullptr;
+}
+
 template <typename S>
-GemvFn<S> gemv_instance(int cw) {
-    if (cw == 16) return &gemv_lds_kernel<S, 16, kBlock>;
-    if (cw == 32) return &gemv_lds_kernel<S, 32, kBlock>;
-    if (cw == 64) return &gemv_lds_kernel<S, 64, kBlock>;
+GemvFn<S> gemv_instance(int cw, int block) {
+    if (block == 512) return gemv_instance_nt<S, 512>(cw);
+    if (block == kBlock) return gemv_instance_nt<S, kBlock>(cw);
     return nullptr;
 }
 
@@ -1231,7 +1248,7 @@ hipError_t launch_gemv_t(const Plan& p, const void* w, const void* x, void* y,
         return launch(gemv_scalar_kernel<S>, p.grid, p.block, 0, stream, ev0,
                       ev1, static_cast<const S*>(w), static_cast<const S*>(x),
                       static_cast<S*>(y), k);
-    const GemvFn<S> fn = gemv_instance<S>(p.cw);
+    const GemvFn<S> fn = gemv_instance<S>(p.cw, p.block);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
     return launch(fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),

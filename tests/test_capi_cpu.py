@@ -78,7 +78,7 @@ def test_vector_contract_predicate():
 @pytest.mark.parametrize("n,k,kernel,cw,j,r,block", [
     (4096, 4096, "lds", 64, 2, 2, 512),
     (11008, 4096, "lds", 64, 2, 2, 512),
-    (4096, 11008, "lds", 64, 6, 1, 256),
+    (4096, 11008, "lds", 64, 6, 1, 512),      # 3+ chunks per lane: 512 threads
     (1024, 4096, "lds", 64, 2, 1, 256),
     (4096, 1024, "lds", 32, 1, 1, 256),
     (1, 128, "lds", 16, 1, 1, 256),
@@ -111,6 +111,12 @@ def test_int4_plans_fall_back_to_scalar():
 def test_q8_launch_plans():
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 4096, 4096, 4096, 8192)
     assert (d["kernel"], d["cw"], d["j"], d["r"]) == ("lds", "64", "4", "1")
+    assert (d["block"], d["grid"]) == ("256", "1024")
+    # 8+ chunks per lane and a grid that still covers every CU: 512 threads
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 4096, 11008, 4096, 8192)
+    assert (d["j"], d["block"], d["grid"]) == ("11", "512", "512")
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 1024, 11008, 4096, 8192)
+    assert (d["j"], d["block"], d["grid"]) == ("11", "256", "256")
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 16, 13, 4096, 8192)
     assert d["kernel"] == "scalar" and d["fallback"] == "1"
     d = _capi.describe_launch("qgemv", "qgemv_wave_r4", 64, 4096, 4096, 8192)
@@ -177,21 +183,22 @@ def test_grouped_argument_errors_without_launch():
 
 
 
-@pytest.mark.parametrize("op,n,k,kernel,cw,j", [
-    ("gemv_f16", 4096, 4096, "lds", 64, 8),
-    ("gemv_f32", 4096, 4096, "lds", 64, 16),
-    ("gemv_f16", 4096, 11008, "lds", 64, 22),
-    ("gemv_f32", 11008, 4096, "lds", 64, 16),
-    ("gemv_f16", 7, 64, "lds", 16, 1),
-    ("gemv_f32", 4096, 16384, "scalar", 0, 0),    # x above the LDS limit
-    ("gemv_f16", 16, 13, "scalar", 0, 0),         # K % 8 != 0
+@pytest.mark.parametrize("op,n,k,kernel,cw,j,block", [
+    ("gemv_f16", 4096, 4096, "lds", 64, 8, 512),
+    ("gemv_f32", 4096, 4096, "lds", 64, 16, 512),
+    ("gemv_f16", 4096, 11008, "lds", 64, 22, 512),
+    ("gemv_f32", 11008, 4096, "lds", 64, 16, 512),
+    ("gemv_f16", 1024, 4096, "lds", 64, 8, 256),   # 512 would leave CUs idle
+    ("gemv_f16", 7, 64, "lds", 16, 1, 256),
+    ("gemv_f32", 4096, 16384, "scalar", 0, 0, 0),    # x above the LDS limit
+    ("gemv_f16", 16, 13, "scalar", 0, 0, 0),         # K % 8 != 0
 ])
-def test_gemv_launch_plans(op, n, k, kernel, cw, j):
+def test_gemv_launch_plans(op, n, k, kernel, cw, j, block):
     d = _capi.describe_launch(op, "gemv_cdna4", n, k, 4096, 8192)
     assert (d["kernel"], int(d["cw"]), int(d["j"])) == (kernel, cw, j)
     if kernel == "lds":
-        assert d["fallback"] == "0" and int(d["block"]) == 256
-        assert int(d["grid"]) == -(-n // ((64 // cw) * 4))
+        assert d["fallback"] == "0" and int(d["block"]) == block
+        assert int(d["grid"]) == -(-n // ((64 // cw) * (block // 64)))
     else:
         assert d["fallback"] == "1"
 
