@@ -712,14 +712,16 @@ __global__ __launch_bounds__(kBlock) void gemv_scalar_kernel(
 // runs with a bounded register budget.
 constexpr int kGemvBatch = 8;
 
-template <typename S, int CW, int NT>
+// JB: chunks per lane per register batch, the smaller of kGemvBatch and
+// the lane's chunk count rounded up to a power of two (a batch longer than
+// the row would load and multiply padding).
+template <typename S, int CW, int NT, int JB>
 __global__ __launch_bounds__(NT) void gemv_lds_kernel(
         const uint4* __restrict__ w,   // [n][nchunks] 16-byte chunks
         const uint4* __restrict__ x,   // [nchunks] 16-byte chunks
         S* __restrict__ y, int n, int nchunks) {
     extern __shared__ uint4 xs[];
     constexpr int SLOTS = 64 / CW;
-    constexpr int JB = kGemvBatch;
     constexpr int XB = 4;              // x chunks per thread per staging pass
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1225,18 +1227,25 @@ namespace {
 template <typename S>
 using GemvFn = void (*)(const uint4*, const uint4*, S*, int, int);
 
-template <typename S, int NT>
+template <typename S, int NT, int JB>
 GemvFn<S> gemv_instance_nt(int cw) {
-    if (cw == 16) return &gemv_lds_kernel<S, 16, NT>;
-    if (cw == 32) return &gemv_lds_kernel<S, 32, NT>;
-    if (cw == 64) return &gemv_lds_kernel<S, 64, NT>;
+    if (cw == 16) return &gemv_lds_kernel<S, 16, NT, JB>;
+    if (cw == 32) return &gemv_lds_kernel<S, 32, NT, JB>;
+    if (cw == 64) return &gemv_lds_kernel<S, 64, NT, JB>;
     return nullptr;
 }
 
+template <typename S, int NT>
+GemvFn<S> gemv_instance_jb(int cw, int j) {
+    if (j <= 2) return gemv_instance_nt<S, NT, 2>(cw);
+    if (j <= 4) return gemv_instance_nt<S, NT, 4>(cw);
+    return gemv_instance_nt<S, NT, kGemvBatch>(cw);
+}
+
 template <typename S>
-GemvFn<S> gemv_instance(int cw, int block) {
-    if (block == 512) return gemv_instance_nt<S, 512>(cw);
-    if (block == kBlock) return gemv_instance_nt<S, kBlock>(cw);
+GemvFn<S> gemv_instance(int cw, int j, int block) {
+    if (block == 512) return gemv_instance_jb<S, 512>(cw, j);
+    if (block == kBlock) return gemv_instance_jb<S, kBlock>(cw, j);
     return nullptr;
 }
 
@@ -1248,7 +1257,7 @@ hipError_t launch_gemv_t(const Plan& p, const void* w, const void* x, void* y,
         return launch(gemv_scalar_kernel<S>, p.grid, p.block, 0, stream, ev0,
                       ev1, static_cast<const S*>(w), static_cast<const S*>(x),
                       static_cast<S*>(y), k);
-    const GemvFn<S> fn = gemv_instance<S>(p.cw, p.block);
+    const GemvFn<S> fn = gemv_instance<S>(p.cw, p.j, p.block);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
     return launch(fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),
