@@ -23,7 +23,10 @@ torch.cuda.synchronize() on both sides.
                 launch (cq_read_ceiling) over an equally cold pool, timed
                 the same way: what one launch of this size can reach.
   cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
-                on the same shape, median of 20 calls, timed on this host
+                on the same shape, median of 20 calls, timed on this host;
+                beside it the same C port on one thread, the reference's
+                torch CPU formulation (dequantize, FP32 torch.mv) on all
+                threads and on one, and the host CPU model
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -129,12 +132,63 @@ def cpu_baseline(N: int, K: int, sets) -> dict:
     from cudalab_amd.operators.int4gemv import int4_bytes
     ex, S = orc.exact_w4(wpn, sn, xn)
     assert orc.arith_ratio(y, ex, S, K).max() <= 1.0
+    one = _median_us(lambda: orc.gemv_w4_cpu(wpn, sn, xn, 1), 5)
+    torch_all, torch_one = _torch_cpu_us(wp.cpu(), s.cpu(), x.cpu(), threads)
     return {"value": round(int4_bytes(N, K) / med / 1e9, 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
             "sample": f"20 calls (after 3 warmup) of the INT4 {N}x{K} GEMV "
                       f"on one input set, median {med * 1e6:.1f} us; fused "
                       f"unpack-dequant-dot in C + OpenMP",
-            "us_per_call": round(med * 1e6, 2)}
+            "us_per_call": round(med * 1e6, 2),
+            "c_port_1_thread_us": round(one, 1),
+            "torch_formulation_us": {"threads": threads, "all_threads": round(torch_all, 1),
+                                     "one_thread": round(torch_one, 1),
+                                     "what": "dequantize_w(W_packed, scale) then "
+                                             "torch.mv(Wd, x.float()).half() on the CPU "
+                                             "(cudalab/int4gemv_correctness.py:220-221), "
+                                             "median of 5 calls after 1 warmup"},
+            "host": _host_cpu()}
+
+
+def _median_us(fn, n: int) -> float:
+    fn()
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e6
+
+
+def _torch_cpu_us(wp, s, x, threads: int) -> tuple[float, float]:
+    """The reference's CPU path (dequantize then an FP32 torch.mv) with
+    `threads` threads and with one."""
+    import torch
+    from cudalab_amd.int4gemv_quantize import dequantize_w
+
+    def call():
+        torch.mv(dequantize_w(wp, s), x.float()).half()
+    prev = torch.get_num_threads()
+    try:
+        torch.set_num_threads(threads)
+        many = _median_us(call, 5)
+        torch.set_num_threads(1)
+        single = _median_us(call, 5)
+    finally:
+        torch.set_num_threads(prev)
+    return many, single
+
+
+def _host_cpu() -> dict:
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count()}
 
 
 def load_traffic(N: int, K: int):
