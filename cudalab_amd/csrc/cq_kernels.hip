@@ -786,7 +786,12 @@ __global__ __launch_bounds__(NT) void gemv_lds_kernel(
 
 // ------------------------------------------------- read-only ceiling
 //
-// A plain streaming read of `bytes` (16-byte loads, 4 per thread).  The
+// A plain streaming read of `bytes`, one 16-byte load per thread.  Of the
+// read patterns measured for one 8.67 MB launch over an HBM-cold pool (1, 2,
+// 4, 8 or 16 loads per thread at 256, 512 or 1024 threads, strided or
+// contiguous, with and without the nontemporal hint), one load per thread
+// in 256-thread workgroups was fastest (2.89 us; 4 loads per thread 3.18 us,
+// 16 loads 3.49 us): the most waves, each with the shortest dependency.  The
 // loaded words are folded and compared with `key`, a launch argument the
 // compiler cannot see, so the loads cannot be removed; the store to `sink`
 // runs only if a thread's fold equals the key (harmless either way: sink is
@@ -795,17 +800,9 @@ __global__ __launch_bounds__(NT) void gemv_lds_kernel(
 __global__ __launch_bounds__(kBlock) void stream_read_kernel(
         const uint4* __restrict__ p, uint32_t* __restrict__ sink, int64_t n16,
         uint32_t key) {
-    constexpr int PER = 4;
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlock * PER + threadIdx.x;
-    uint4 v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int64_t idx = base + static_cast<int64_t>(i) * kBlock;
-        v[i] = p[idx < n16 ? idx : n16 - 1];
-    }
-    uint32_t a = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) a ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const uint4 v = p[idx < n16 ? idx : n16 - 1];
+    const uint32_t a = v.x ^ v.y ^ v.z ^ v.w;
     if (a == key) sink[0] = a;
 }
 
@@ -1278,7 +1275,7 @@ hipError_t launch_gemv(const Plan& p, int dtype, const void* w, const void* x,
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
                               hipStream_t stream) {
     const int64_t n16 = bytes / 16;
-    const int64_t grid = (n16 + kBlock * 4 - 1) / (kBlock * 4);
+    const int64_t grid = (n16 + kBlock - 1) / kBlock;
     return launch(stream_read_kernel, grid, kBlock, 0, stream, nullptr,
                   nullptr, static_cast<const uint4*>(buf),
                   static_cast<uint32_t*>(sink), n16, 0x9E3779B9u);
