@@ -349,7 +349,8 @@ int cq_quantize_vectorized(int op, const void* w, const void* out, int64_t n,
                            int64_t k) {
     if (op == CQ_OP_INT4GEMV) return cq::plan_int4_quantize(n, k, w, out).fast ? 1 : 0;
     if (op == CQ_OP_QGEMV) return cq::plan_q8_quantize(n, k, w, out).fast ? 1 : 0;
-    return fail(CQ_ERR_INVALID_ARG, "quantizers exist for CQ_OP_INT4GEMV and CQ_OP_QGEMV only"), -1;
+    fail(CQ_ERR_INVALID_ARG, "quantizers exist for CQ_OP_INT4GEMV and CQ_OP_QGEMV only");
+    return -1;
 }
 
 int cq_native_timing(int op, const char* variant, const void* w,

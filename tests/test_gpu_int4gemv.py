@@ -19,8 +19,10 @@ BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
 # (4099, 4096): two rows per lane on 512-thread workgroups with a partial
 # last workgroup and a grid (257) that is not a multiple of the 8 XCDs
+# (4099, 4096) and (4097, 11008): partial last workgroups of the 512-thread
+# plans (two rows per lane; 3+ chunks per lane)
 EXTRA = [(5, 16384), (7, 16512), (1, 2048), (65, 384), (300, 1280),
-         (4099, 4096)]
+         (4099, 4096), (4097, 11008)]
 
 
 def _np(t: torch.Tensor) -> np.ndarray:

@@ -16,8 +16,9 @@ EDGE = [(1, 1), (1, 4096), (4096, 1), (16, 13), (8, 7)]
 BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
 # (1001, 4096): a grid (251 workgroups) that is not a multiple of the 8 XCDs
+# (4097, 11008): partial last workgroup of a 512-thread plan (8+ chunks per lane)
 EXTRA = [(5, 16384), (3, 16400), (17, 16), (9, 48), (300, 1040), (2, 8192),
-         (1001, 4096)]
+         (1001, 4096), (4097, 11008)]
 
 
 def _np(t):
