@@ -22,6 +22,9 @@ torch.cuda.synchronize() on both sides.
                 `measured_ceiling` is a plain read of the same bytes per
                 launch (cq_read_ceiling) over an equally cold pool, timed
                 the same way: what one launch of this size can reach.
+                `launch_floor_us` is an empty kernel of the GEMV's grid and
+                workgroup size (cq_launch_floor), timed the same way: the
+                per-dispatch cost inside every call.
   cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
                 on the same shape, median of 20 calls, timed on this host;
                 beside it the same C port on one thread, the reference's
@@ -262,8 +265,9 @@ def main(argv=None) -> int:
 
     r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup)
 
-    from cudalab_amd.ext import read_ceiling
+    from cudalab_amd.ext import launch_floor, read_ceiling
     ceil = read_ceiling(nbytes)
+    floor_us = launch_floor(int(plan["grid"]), int(plan["block"]))
 
     total_s = r["total_us"] * 1e-6
     value = nbytes * args.steps / total_s / 1e9
@@ -329,7 +333,14 @@ def main(argv=None) -> int:
                      "ceiling_note": "plain streaming read of the same bytes "
                                      "per launch over an HBM-cold pool "
                                      "(cq_read_ceiling), same timed-window "
-                                     "caliber"},
+                                     "caliber",
+                     "launch_floor_us": round(floor_us, 4),
+                     "floor_note": "back-to-back launches of a kernel with no "
+                                   "memory work in the GEMV's launch shape "
+                                   "(cq_launch_floor, grid %s x %s threads), "
+                                   "same caliber: the per-dispatch cost "
+                                   "included in us_per_call" % (plan["grid"],
+                                                                plan["block"])},
         "cpu_baseline": cpu,
         "detail": detail,
     }

@@ -504,6 +504,37 @@ int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
     return CQ_OK;
 }
 
+int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
+                    int64_t warmup, int64_t n_launches, double* total_us) {
+    g_last_error.clear();
+    if (sink == nullptr || total_us == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null argument");
+    if (warmup < 0 || n_launches < 1)
+        return fail(CQ_ERR_INVALID_ARG, "n_launches must be >= 1, warmup >= 0");
+    if (grid < 1 || grid > INT_MAX || block < 1 || block > 1024)
+        return fail(CQ_ERR_INVALID_ARG,
+                    "grid must be in [1, INT_MAX] and block in [1, 1024]");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    for (int64_t i = 0; i < warmup; ++i)
+        if ((e = cq::launch_empty(grid, block, sink, s)) != hipSuccess)
+            return hip_fail(e, "warmup launch");
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    Events win;
+    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    for (int64_t i = 0; i < n_launches; ++i)
+        if ((e = cq::launch_empty(grid, block, sink, s)) != hipSuccess)
+            return hip_fail(e, "timed launch");
+    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
+        return hip_fail(e, "hipEventElapsedTime");
+    *total_us = static_cast<double>(ms) * 1e3;
+    return CQ_OK;
+}
+
 int cq_variants(int op, int which, char* buf, size_t cap) {
     g_last_error.clear();
     if (!valid_op(op))

@@ -108,4 +108,9 @@ hipError_t launch_q8_quantize(const QuantPlan& p, const void* w, void* wq,
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
                               hipStream_t stream);
 
+// One launch of a kernel with no memory work, `grid` workgroups of `block`
+// threads (1..1024): the per-dispatch cost of that launch shape.
+hipError_t launch_empty(int64_t grid, int block, void* sink,
+                        hipStream_t stream);
+
 }  // namespace cq

@@ -806,6 +806,16 @@ __global__ __launch_bounds__(kBlock) void stream_read_kernel(
     if (a == key) sink[0] = a;
 }
 
+// A workgroup that does no memory work: launched back to back on one stream
+// it measures what one dispatch of a given grid and workgroup size costs
+// before any kernel body runs (command processing, workgroup launch, the
+// end-of-kernel release).  The store is never taken: the host passes a key
+// no thread index reaches.
+__global__ __launch_bounds__(1024) void empty_launch_kernel(
+        uint32_t* __restrict__ sink, uint32_t key) {
+    if (threadIdx.x == key) sink[0] = blockIdx.x;
+}
+
 // --------------------------------------------------------- instance tables
 
 using Int4Fn = void (*)(const uint4*, const uint16_t*, const uint4*,
@@ -1279,6 +1289,12 @@ hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
     return launch(stream_read_kernel, grid, kBlock, 0, stream, nullptr,
                   nullptr, static_cast<const uint4*>(buf),
                   static_cast<uint32_t*>(sink), n16, 0x9E3779B9u);
+}
+
+hipError_t launch_empty(int64_t grid, int block, void* sink,
+                        hipStream_t stream) {
+    return launch(empty_launch_kernel, grid, block, 0, stream, nullptr,
+                  nullptr, static_cast<uint32_t*>(sink), 0xFFFFFFFFu);
 }
 
 }  // namespace cq

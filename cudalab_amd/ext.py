@@ -626,6 +626,24 @@ def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
             "pool_buffers": n}
 
 
+def launch_floor(grid: int, block: int, warmup: int = 200,
+                 n_launches: int = 2000, device: str = "cuda") -> float:
+    """µs per launch of a kernel with no memory work, `grid` workgroups of
+    `block` threads, back to back on the current stream (cq_launch_floor):
+    the per-dispatch cost of that launch shape in the pool-timing caliber."""
+    lib = _capi.load()
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    tot = ctypes.c_double(0.0)
+    with torch.cuda.device(sink.device):
+        s = torch.cuda.current_stream(sink.device)
+        st = lib.cq_launch_floor(int(grid), int(block), sink.data_ptr(),
+                                 s.cuda_stream, warmup, n_launches,
+                                 ctypes.byref(tot))
+    if st != _capi.CQ_OK:
+        _fail(f"launch_floor failed (status {st}): {_capi.last_error()}")
+    return tot.value / n_launches
+
+
 # ---------------------------------------------------------------- quantizers
 def _quant_launch(fn, what: str, W: torch.Tensor, q: torch.Tensor,
                   scale: torch.Tensor, rcp: bool) -> None:

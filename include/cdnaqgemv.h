@@ -243,6 +243,19 @@ int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
                     int64_t n_launches, double* total_us);
 
 /*
+ * Launch floor: `n_launches` back-to-back launches of a kernel that does no
+ * memory work, `grid` workgroups (1..INT_MAX) of `block` threads (1..1024),
+ * after `warmup` untimed launches; *total_us receives the event time of the
+ * timed window.  `sink` is a device buffer of at least 4 bytes (never
+ * written).  No counterpart in the reference: it measures what one dispatch
+ * of a GEMV's launch shape costs on this device before any kernel body
+ * runs, the part of a call's time that no kernel change can remove.
+ * Synchronizes the stream.
+ */
+int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
+                    int64_t warmup, int64_t n_launches, double* total_us);
+
+/*
  * Variant names of `op`, sorted, '\n'-separated, NUL-terminated, written to
  * buf (capacity cap).  which = CQ_LIST_NORMAL (dispatchable),
  * CQ_LIST_ALL (also quarantined), CQ_LIST_QUARANTINED, or CQ_LIST_ALIASES

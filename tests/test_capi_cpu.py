@@ -27,6 +27,7 @@ def _declared_functions() -> set[str]:
 def test_header_declares_the_abi():
     names = _declared_functions()
     assert {"cq_int4gemv", "cq_qgemv", "cq_native_timing", "cq_pool_timing", "cq_read_ceiling",
+            "cq_launch_floor",
             "cq_int4gemv_grouped", "cq_qgemv_grouped", "cq_gemv",
             "cq_variants", "cq_vec_contract_ok", "cq_describe_launch",
             "cq_last_error", "cq_version"} <= names
@@ -156,6 +157,13 @@ def test_argument_errors_without_launch():
     assert st == _capi.CQ_ERR_INVALID_ARG
     st = lib.cq_read_ceiling(bufs, 1, 4096, None, None, 0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()
+    st = lib.cq_launch_floor(256, 512, None, None, 0, 1, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()
+    st = lib.cq_launch_floor(256, 512, P, None, 0, 0, ctypes.byref(tot))
+    assert st == _capi.CQ_ERR_INVALID_ARG and "n_launches" in _capi.last_error()
+    for grid, block in ((0, 256), (1 << 31, 256), (256, 0), (256, 1025)):
+        st = lib.cq_launch_floor(grid, block, P, None, 0, 1, ctypes.byref(tot))
+        assert st == _capi.CQ_ERR_INVALID_ARG and "grid must be" in _capi.last_error()
 
 
 def test_grouped_argument_errors_without_launch():

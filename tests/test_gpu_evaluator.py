@@ -69,3 +69,21 @@ def test_bench_matrix_cell(op4, ext4):
     assert set(rec["per_variant"]) == set(variants)
     with pytest.raises(ValueError, match="unknown variant"):
         bench_matrix(op4, ext4, ["int4gemv_cdna4", "no_such"], 64, 128, **FAST)
+
+
+def test_launch_floor_and_read_ceiling(ext4):
+    """The two reference points the bench reports beside a GEMV call: the
+    empty-launch floor of the GEMV's launch shape, and the plain read of the
+    same bytes.  A read does strictly more than an empty launch, so its time
+    per call is the larger; both are small positive numbers."""
+    from cudalab_amd import ext as E
+    announce("launch_floor 256x512")
+    floor = E.launch_floor(256, 512, warmup=50, n_launches=500)
+    announce("read_ceiling 8667136 B")
+    ceil = E.read_ceiling(8667136, warmup=50, n_launches=500)
+    assert 0 < floor < 50.0
+    assert 0 < ceil["us_per_call"] < 50.0
+    assert floor < 2 * ceil["us_per_call"]
+    for grid, block in ((0, 256), (256, 0), (256, 1025)):
+        with pytest.raises(RuntimeError, match="grid must be"):
+            E.launch_floor(grid, block, warmup=0, n_launches=1)
