@@ -27,3 +27,19 @@ def test_profile_variant(cuda, tmp_path):
     assert s["algorithmic_bw_gbps"] > 0
     assert s["counters"]["FETCH_SIZE"] is not None and s["counters"]["FETCH_SIZE"] > 0
     assert (tmp_path / "summary.json").exists()
+
+
+def test_cli_profile(cuda, tmp_path, capsys):
+    from cudalab_amd import cli
+    from cudalab_amd.evaluator.profiler import rocprof_path
+    if rocprof_path() is None:
+        pytest.skip("rocprofv3 not installed")
+    announce("cli profile qgemv --variants qgemv_cdna4 1024x4096 --counters FETCH_SIZE")
+    rc = cli.main(["profile", "qgemv", "--variants", "qgemv_cdna4", "--M", "1024",
+                   "--H", "4096", "--counters", "FETCH_SIZE", "--out-dir", str(tmp_path)])
+    assert rc == 0
+    import json
+    s = json.loads((tmp_path / "qgemv_cdna4_M1024_H4096" / "summary.json").read_text())
+    assert s["kernels"] and s["kernel_duration_us"] > 0, s["errors"]
+    assert s["counters"]["FETCH_SIZE"] and s["clock_control"]["applied"] is False
+    assert "duration=" in capsys.readouterr().out
