@@ -22,6 +22,7 @@
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace {
@@ -120,6 +121,49 @@ const Variant* find_variant(int op, const char* name) {
     return nullptr;
 }
 
+// Byte ranges of one problem's operands (w, scale, x, y), for the overlap
+// checks.  A kernel reads w, scale and x while other workgroups already
+// write y, so y must not share a byte with them; in a grouped launch no
+// problem's y may share a byte with any operand of another problem either.
+// gemv has no scale (empty range).  Sizes are computed in 128 bits: n and
+// k are at most 2^31 - 1, so no product overflows.
+struct Span {
+    unsigned __int128 lo = 0, hi = 0;
+};
+
+bool overlaps(const Span& a, const Span& b) {
+    return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi;
+}
+
+struct Operands {
+    Span w, scale, x, y;
+};
+
+Operands operand_spans(int op, const void* w, const void* scale, const void* x,
+                       const void* y, int64_t n, int64_t k) {
+    using U = unsigned __int128;
+    const U un = static_cast<U>(n), uk = static_cast<U>(k);
+    U wb, sb = 0, xe = 2, ye = 2;
+    if (op == CQ_OP_INT4GEMV) {
+        wb = un * uk / 2;
+        sb = un * (uk / 128) * 2;
+    } else if (op == CQ_OP_QGEMV) {
+        wb = un * uk;
+        sb = un * 4;
+    } else {
+        xe = ye = op == CQ_OP_GEMV_F32 ? 4 : 2;
+        wb = un * uk * xe;
+    }
+    auto span = [](const void* p, U bytes) {
+        Span r;
+        r.lo = reinterpret_cast<uintptr_t>(p);
+        r.hi = r.lo + bytes;
+        return r;
+    };
+    return {span(w, wb), span(scale, scale != nullptr ? sb : 0), span(x, uk * xe),
+            span(y, un * ye)};
+}
+
 // Shared pre-launch checks of both operators.  Returns CQ_OK or a status
 // with the message set.
 int check_call(int op, const char* variant, const Variant** out,
@@ -145,6 +189,25 @@ int check_call(int op, const char* variant, const Variant** out,
                     "k must be divisible by 128 (group_size=128), got " + std::to_string(k));
     *out = v;
     return CQ_OK;
+}
+
+// The output of a call must not share a byte with its inputs.  Run after
+// check_call by every entry point that launches.
+int check_disjoint(int op, const void* w, const void* scale, const void* x,
+                   const void* y, int64_t n, int64_t k) {
+    const Operands o = operand_spans(op, w, is_gemv(op) ? nullptr : scale, x, y, n, k);
+    if (overlaps(o.y, o.w) || overlaps(o.y, o.scale) || overlaps(o.y, o.x))
+        return fail(CQ_ERR_INVALID_ARG,
+                    "output y overlaps an input (w, scale or x) of the same call");
+    return CQ_OK;
+}
+
+// check_call, then check_disjoint.
+int check_launch(int op, const char* variant, const Variant** out,
+                 const void* w, const void* scale, const void* x,
+                 const void* y, int64_t n, int64_t k) {
+    const int st = check_call(op, variant, out, w, scale, x, y, n, k);
+    return st != CQ_OK ? st : check_disjoint(op, w, scale, x, y, n, k);
 }
 
 int gemv_dtype(int op) { return op == CQ_OP_GEMV_F32 ? cq::kF32 : cq::kF16; }
@@ -176,7 +239,7 @@ int run_one(int op, const char* variant, const void* w, const void* scale,
             const void* x, void* y, int64_t n, int64_t k, void* stream) {
     g_last_error.clear();
     const Variant* v = nullptr;
-    const int st = check_call(op, variant, &v, w, scale, x, y, n, k);
+    const int st = check_launch(op, variant, &v, w, scale, x, y, n, k);
     if (st != CQ_OK) return st;
     const cq::Plan p = make_plan(op, *v, n, k, w, x);
     const hipError_t e = launch_plan(op, p, w, scale, x, y, n, k,
@@ -216,10 +279,47 @@ int run_grouped(int op, const char* variant, const cq_gemv_problem_t* probs,
     const Variant* v = nullptr;
     for (int64_t i = 0; i < count; ++i) {
         const cq_gemv_problem_t& q = probs[i];
-        const int st = check_call(op, variant, &v, q.w, q.scale, q.x, q.y, q.n, k);
+        const int st = check_launch(op, variant, &v, q.w, q.scale, q.x, q.y, q.n, k);
         if (st != CQ_OK) {
             g_last_error = "problem " + std::to_string(i) + ": " + g_last_error;
             return st;
+        }
+    }
+    // Problems of one launch run concurrently: no output may share a byte
+    // with another problem's operands or output (inputs may be shared, as
+    // q/k/v share x).  The outputs are sorted by address: adjacent ones
+    // must not overlap, and then each input span is looked up among them.
+    std::vector<Operands> ops(static_cast<size_t>(count));
+    std::vector<int64_t> by_y(static_cast<size_t>(count));
+    for (int64_t i = 0; i < count; ++i) {
+        const cq_gemv_problem_t& q = probs[i];
+        ops[static_cast<size_t>(i)] = operand_spans(op, q.w, q.scale, q.x, q.y, q.n, k);
+        by_y[static_cast<size_t>(i)] = i;
+    }
+    auto ys = [&](int64_t i) -> const Span& { return ops[static_cast<size_t>(i)].y; };
+    std::sort(by_y.begin(), by_y.end(),
+              [&](int64_t a, int64_t b) { return ys(a).lo < ys(b).lo; });
+    auto conflict = [&](int64_t i, const char* what, int64_t j) {
+        return fail(CQ_ERR_INVALID_ARG,
+                    "problem " + std::to_string(i) + ": output y overlaps " + what +
+                        " of problem " + std::to_string(j) +
+                        " (the problems of a grouped call must be independent)");
+    };
+    for (size_t t = 1; t < by_y.size(); ++t)
+        if (overlaps(ys(by_y[t - 1]), ys(by_y[t])))
+            return conflict(by_y[t], "y", by_y[t - 1]);
+    for (int64_t j = 0; j < count; ++j) {
+        const Operands& o = ops[static_cast<size_t>(j)];
+        const std::pair<const Span*, const char*> inputs[] = {
+            {&o.w, "w"}, {&o.scale, "scale"}, {&o.x, "x"}};
+        for (const auto& [sp, what] : inputs) {
+            // first output ending after the input starts; outputs are
+            // disjoint, so their ends are sorted too
+            auto it = std::partition_point(by_y.begin(), by_y.end(), [&](int64_t i) {
+                return ys(i).hi <= sp->lo;
+            });
+            for (; it != by_y.end() && ys(*it).lo < sp->hi; ++it)
+                if (*it != j && overlaps(ys(*it), *sp)) return conflict(*it, what, j);
         }
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -364,7 +464,7 @@ int cq_native_timing(int op, const char* variant, const void* w,
     if (launches_per_window < 1)
         return fail(CQ_ERR_INVALID_ARG, "launches_per_window must be >= 1");
     const Variant* v = nullptr;
-    int st = check_call(op, variant, &v, w, scale, x, y, n, k);
+    int st = check_launch(op, variant, &v, w, scale, x, y, n, k);
     if (st != CQ_OK) return st;
     const cq::Plan p = make_plan(op, *v, n, k, w, x);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -425,7 +525,7 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
     const Variant* v = nullptr;
     for (int64_t i = 0; i < n_sets; ++i) {
         const void* sc = scale != nullptr ? scale[i] : nullptr;
-        const int st = check_call(op, variant, &v, w[i], sc, x[i], y[i], n, k);
+        const int st = check_launch(op, variant, &v, w[i], sc, x[i], y[i], n, k);
         if (st != CQ_OK) return st;
         plans[static_cast<size_t>(i)] = make_plan(op, *v, n, k, w[i], x[i]);
     }

@@ -96,6 +96,9 @@ extern "C" {
  * `int4gemv_forward` / `int4gemv_forward_into`
  * (kernels/int4gemv/bindings.cpp:145-176).  `variant` is a name from
  * cq_variants(CQ_OP_INT4GEMV, ...), e.g. "int4gemv_baseline".
+ * For this and every other launching entry point, y must not share a byte
+ * with w, scale or x of the same call (CQ_ERR_INVALID_ARG, nothing
+ * launched): workgroups write y while others still read the inputs.
  */
 int cq_int4gemv(const char* variant, const void* w_packed, const void* scale,
                 const void* x, void* y, int64_t n, int64_t k, void* stream);
@@ -134,7 +137,10 @@ typedef struct cq_gemv_problem {
  * in which a problem misses the vector contract, launch problem by
  * problem).  Each y is bit-identical to a cq_int4gemv / cq_qgemv call of
  * the same variant on the same problem.  Every problem is checked as a
- * single call would be before anything is launched.  No counterpart in the
+ * single call would be before anything is launched.  The problems run at
+ * the same time, so no problem's y may share a byte with another problem's
+ * w, scale, x or y (CQ_ERR_INVALID_ARG naming both problems); inputs may be
+ * shared (q/k/v read one x).  No counterpart in the
  * reference (its variants launch one problem at a time): it serves decode
  * steps whose projections are independent (q/k/v; gate/up) and pays the
  * per-launch cost once per batch.

@@ -166,13 +166,23 @@ def test_argument_errors_without_launch():
         assert st == _capi.CQ_ERR_INVALID_ARG and "grid must be" in _capi.last_error()
 
 
+def _disjoint_problems(count, n=8):
+    """Problems with non-overlapping fake device addresses (never launched:
+    every call below fails its argument checks first)."""
+    probs = (_capi.CqProblem * count)()
+    for i in range(count):
+        probs[i].w = 0x10000000 + i * 0x1000000
+        probs[i].scale = probs[i].w + 0x800000
+        probs[i].x = 0x70000000 + i * 0x10000
+        probs[i].y = 0x80000000 + i * 0x10000
+        probs[i].n = n
+    return probs
+
+
 def test_grouped_argument_errors_without_launch():
     lib = _capi.load()
-    P = 0x1000
-    probs = (_capi.CqProblem * 3)()
-    for i in range(3):
-        probs[i].w = probs[i].scale = probs[i].x = probs[i].y = P
-        probs[i].n = 8
+    P = 0x80000000
+    probs = _disjoint_problems(3)
     st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", None, 1, 128, None)
     assert st == _capi.CQ_ERR_INVALID_ARG and "NULL" in _capi.last_error()
     st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 0, 128, None)
@@ -184,10 +194,61 @@ def test_grouped_argument_errors_without_launch():
     probs[1].y = None
     st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 3, 128, None)
     assert st == _capi.CQ_ERR_INVALID_ARG and _capi.last_error().startswith("problem 1:")
-    probs[1].y = P
+    probs[1].y = P + 0x10000
     probs[2].n = 0
     st = lib.cq_qgemv_grouped(b"qgemv_cdna4", probs, 3, 16, None)
     assert st == _capi.CQ_ERR_INVALID_ARG and _capi.last_error().startswith("problem 2:")
+
+
+def test_output_overlap_is_rejected_before_launch():
+    """A kernel reads w, scale and x while other workgroups already write y,
+    and the problems of a grouped launch run at the same time: an output
+    sharing a byte with an input of its own call, or with any operand of
+    another problem of the same grouped call, is an argument error.  Inputs
+    may be shared (q/k/v read one x).  Nothing here reaches a launch."""
+    lib = _capi.load()
+    w, sc, x = 0x10000000, 0x20000000, 0x30000000       # k = 128: x is 256 bytes
+    for y in (x, x + 254, w + 100, sc):
+        st = lib.cq_int4gemv(b"int4gemv_cdna4", w, sc, x, y, 8, 128, None)
+        assert st == _capi.CQ_ERR_INVALID_ARG, hex(y)
+        assert "overlaps an input" in _capi.last_error()
+    st = lib.cq_qgemv(b"qgemv_cdna4", w, sc, x, sc + 31, 8, 16, None)    # scale: 32 B
+    assert st == _capi.CQ_ERR_INVALID_ARG and "overlaps" in _capi.last_error()
+    st = lib.cq_gemv(b"gemv_cdna4", _capi.CQ_DTYPE_F32, w, x, x + 16 * 4 - 4, 2, 16, None)
+    assert st == _capi.CQ_ERR_INVALID_ARG and "overlaps" in _capi.last_error()
+    # grouped: y of one problem inside another problem's x, w, scale or y
+    cases = [("x", lambda p: setattr(p[1], "y", p[0].x + 2)),
+             ("w", lambda p: setattr(p[2], "y", p[0].w + 64)),
+             ("scale", lambda p: setattr(p[0], "y", p[2].scale)),
+             ("y", lambda p: setattr(p[1], "y", p[2].y + 8))]
+    for what, plant in cases:
+        probs = _disjoint_problems(3)
+        plant(probs)
+        st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, 3, 128, None)
+        assert st == _capi.CQ_ERR_INVALID_ARG, what
+        msg = _capi.last_error()
+        assert f"output y overlaps {what} of problem" in msg, msg
+        assert "must be independent" in msg
+
+
+def test_grouped_overlap_check_scales_and_allows_shared_inputs(monkeypatch):
+    """Many problems sharing one x (allowed) with one planted conflict at
+    the end: the sorted check finds it without a quadratic scan."""
+    lib = _capi.load()
+    count = 20000
+    probs = _disjoint_problems(count, n=8)
+    for i in range(count):
+        probs[i].x = 0x70000000                        # shared input
+        probs[i].w = 0x100000000 + i * 0x1000
+        probs[i].scale = 0x300000000 + i * 0x100
+        probs[i].y = 0x500000000 + i * 0x100
+    probs[count - 1].y = probs[3].w + 16                # conflict: y inside w of problem 3
+    import time
+    t0 = time.perf_counter()
+    st = lib.cq_int4gemv_grouped(b"int4gemv_cdna4", probs, count, 128, None)
+    assert time.perf_counter() - t0 < 5.0
+    assert st == _capi.CQ_ERR_INVALID_ARG
+    assert _capi.last_error().startswith(f"problem {count - 1}: output y overlaps w of problem 3")
 
 
 

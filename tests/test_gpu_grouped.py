@@ -113,3 +113,28 @@ def test_q8_grouped_odd_k_falls_back(ext8):
     outs = _check(ext8, "qgemv_cdna4", probs)
     for (W, s, x), y in zip(probs, outs):
         assert torch.equal(y, ext8.forward("qgemv_baseline", W, s, x))
+
+
+def test_grouped_rejects_dependent_problems(ext4, ext8):
+    """The problems of one grouped launch run at the same time, so one
+    problem's output may not be another's input or output (that chain needs
+    two calls).  Shared inputs stay allowed: q/k/v read one x.  Nothing is
+    launched for a rejected call: the outputs keep their contents."""
+    announce("grouped overlap rejection int4/int8")
+    wp0, s0, x = _int4_problem(256, 1024, seed=61)
+    wp1, s1, x1 = _int4_problem(1024, 1024, seed=62)
+    y0 = torch.zeros(256, dtype=torch.float16, device="cuda")
+    y1 = torch.zeros(1024, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="problem 1: output y overlaps x of problem 0"):
+        ext4.forward_grouped("int4gemv_cdna4", [(wp0, s0, x, y0), (wp1, s1, x1, x)])
+    with pytest.raises(RuntimeError, match="overlaps"):
+        ext4.forward_grouped("int4gemv_cdna4", [(wp0, s0, x, y1[:256]), (wp1, s1, x, y1)])
+    with pytest.raises(RuntimeError, match="overlaps an input"):
+        ext4.forward_into("int4gemv_cdna4", wp1, s1, x, x)
+    torch.cuda.synchronize()
+    assert not y0.any() and not y1.any()
+    # the same two problems with separate outputs and a shared x are fine
+    _check(ext4, "int4gemv_cdna4", [(wp0, s0, x), (wp1, s1, x)])
+    wq, sq, xq = _q8_problem(512, 512, seed=63)
+    with pytest.raises(RuntimeError, match="overlaps"):
+        ext8.forward_grouped("qgemv_cdna4", [(wq, sq, xq, xq), (wq, sq, xq, torch.empty(512, dtype=torch.float16, device="cuda"))])
