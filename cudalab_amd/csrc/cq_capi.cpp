@@ -267,6 +267,17 @@ int check_quantize(int op, const void* w, const void* q, const void* scale,
         reinterpret_cast<uintptr_t>(scale) % sa != 0)
         return fail(CQ_ERR_INVALID_ARG, "w must be 2-byte aligned and scale aligned "
                                         "to its element size");
+    // The kernels read w while other workgroups write the packed weights
+    // and scales: the three ranges must be disjoint.  operand_spans gives
+    // the packed weights' and scales' ranges for the operator (as "w" and
+    // "scale"); the fp16 input is n * k * 2 bytes.
+    const Operands o = operand_spans(op, q, scale, nullptr, nullptr, n, k);
+    Span in;
+    in.lo = reinterpret_cast<uintptr_t>(w);
+    in.hi = in.lo + static_cast<unsigned __int128>(n) * static_cast<unsigned __int128>(k) * 2;
+    if (overlaps(in, o.w) || overlaps(in, o.scale) || overlaps(o.w, o.scale))
+        return fail(CQ_ERR_INVALID_ARG, "w, the quantized output and scale must not "
+                                        "overlap");
     return CQ_OK;
 }
 

@@ -161,7 +161,8 @@ int cq_qgemv_grouped(const char* variant, const cq_gemv_problem_t* problems,
  * ops, on the CPU (CQ_SCALE_DIV) or on a GPU (CQ_SCALE_RCP).  Asynchronous
  * on `stream`.  NaN/Inf in w is not rejected: the scale of every group
  * holding one is non-finite, and finite w never gives a non-finite scale,
- * so a caller checks the scale.
+ * so a caller checks the scale.  w, w_packed and scale must not overlap
+ * (CQ_ERR_INVALID_ARG; the same holds for cq_q8_quantize).
  */
 int cq_int4_quantize(const void* w, void* w_packed, void* scale, int64_t n,
                      int64_t k, int scale_mode, void* stream);

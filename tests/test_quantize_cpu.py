@@ -296,6 +296,23 @@ def test_quantize_argument_errors_without_launch():
     assert lib.cq_q8_quantize(P, P, Q, 4, 7, -1, None) == E
 
 
+def test_quantize_overlapping_buffers_rejected_without_launch():
+    """The kernels read w while other workgroups write the packed weights
+    and the scales: in-place or overlapping buffers are argument errors
+    (w is n*k*2 bytes; INT4 packed n*k/2 and scale n*(k/128)*2; INT8
+    packed n*k and scale n*4)."""
+    lib = _capi.load()
+    E = _capi.CQ_ERR_INVALID_ARG
+    R = _capi.CQ_SCALE_RCP
+    W, Q, S = 0x100000, 0x200000, 0x300000                # n = 4, k = 128: w 1024 B
+    for w, q, s in ((W, W, S), (W, W + 1020, S), (W, Q, W + 512), (W, Q, Q + 252)):
+        assert lib.cq_int4_quantize(w, q, s, 4, 128, R, None) == E, (hex(w), hex(q), hex(s))
+        assert "must not overlap" in _capi.last_error()
+    for w, q, s in ((W, W + 1016, S), (W, Q, Q + 504)):   # INT8: packed 512 B
+        assert lib.cq_q8_quantize(w, q, s, 4, 128, R, None) == E, (hex(q), hex(s))
+        assert "must not overlap" in _capi.last_error()
+
+
 @pytest.mark.parametrize("op,w,out,n,k,fast", [
     ("int4gemv", 0x1000, 0x2000, 4, 128, True),
     ("int4gemv", 0x1002, 0x2000, 4, 128, False),   # w not 16-byte aligned
