@@ -26,10 +26,12 @@ torch.cuda.synchronize() on both sides.
                 workgroup size (cq_launch_floor), timed the same way: the
                 per-dispatch cost inside every call.
   cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
-                on the same shape, median of 20 calls, timed on this host;
-                beside it the same C port on one thread, the reference's
-                torch CPU formulation (dequantize, FP32 torch.mv) on all
-                threads and on one, and the host CPU model
+                on the same shape, timed on this host over a bounded sample:
+                about --cpu-seconds (6 s) of calls cycling over 16 distinct
+                host-resident sets of the pool, median per call; beside it
+                the same C port on one thread, the reference's torch CPU
+                formulation (dequantize, FP32 torch.mv) on all threads and
+                on one, and the host CPU model (about 13 s of CPU in all)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -59,6 +61,10 @@ def parse_args(argv=None):
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--k", type=int, default=4096)
     ap.add_argument("--mode", choices=("streaming", "hot"), default="streaming")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="CPU baseline sample: seconds of the all-thread C port "
+                         "(half that on one thread, a third per thread count for "
+                         "the torch formulation)")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-detail", action="store_true",
@@ -144,71 +150,91 @@ def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
     return _make_sets(op, N, K, mode, seed)
 
 
-def cpu_baseline(N: int, K: int, sets) -> dict:
-    """Oracle CPU GEMV on one set's inputs copied to host (untimed copy)."""
-    import numpy as np
-    from oracle import oracle as orc
-    wp, s, x, _ = sets[0]
-    wpn = wp.cpu().numpy()
-    sn = s.cpu().numpy()
-    xn = x.cpu().numpy()
-    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or min(16, os.cpu_count() or 1)
-    for _ in range(3):
-        orc.gemv_w4_cpu(wpn, sn, xn, threads)
-    times = []
-    for _ in range(20):
+def _timed_calls(fn, min_s: float, min_n: int, max_n: int) -> list[float]:
+    """Seconds of each call fn(i), i = 0, 1, ..., until at least `min_s`
+    seconds and `min_n` calls have run (at most `max_n` calls)."""
+    ts: list[float] = []
+    t_end = time.perf_counter() + min_s
+    while len(ts) < max_n and (len(ts) < min_n or time.perf_counter() < t_end):
         t0 = time.perf_counter()
-        y = orc.gemv_w4_cpu(wpn, sn, xn, threads)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+        fn(len(ts))
+        ts.append(time.perf_counter() - t0)
+    return ts
+
+
+def cpu_baseline(N: int, K: int, sets, seconds: float = 6.0,
+                 max_sets: int = 16) -> dict:
+    """The oracle's fused C + OpenMP GEMV, timed on this host over a bounded
+    sample of the bench workload: the first `max_sets` sets of the pool,
+    copied to host memory (untimed), cycled call by call for about
+    `seconds` with all threads, then about seconds/2 on one thread.  Beside
+    it the reference's torch CPU formulation, about seconds/3 per thread
+    count.  Medians per call."""
+    from oracle import oracle as orc
     from cudalab_amd.operators.int4gemv import int4_bytes
+    host = [(wp.cpu().numpy(), s.cpu().numpy(), x.cpu().numpy())
+            for (wp, s, x, _) in sets[:max_sets]]
+    m = len(host)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or min(16, os.cpu_count() or 1)
+    wpn, sn, xn = host[0]
+    y = orc.gemv_w4_cpu(wpn, sn, xn, threads)
     ex, S = orc.exact_w4(wpn, sn, xn)
     assert orc.arith_ratio(y, ex, S, K).max() <= 1.0
-    one = _median_us(lambda: orc.gemv_w4_cpu(wpn, sn, xn, 1), 5)
-    torch_all, torch_one = _torch_cpu_us(wp.cpu(), s.cpu(), x.cpu(), threads)
-    return {"value": round(int4_bytes(N, K) / med / 1e9, 3), "unit": "GB/s",
+    for i in range(3):
+        orc.gemv_w4_cpu(*host[i % m], threads)
+    many = _timed_calls(lambda i: orc.gemv_w4_cpu(*host[i % m], threads),
+                        seconds, 20, 200000)
+    one = _timed_calls(lambda i: orc.gemv_w4_cpu(*host[i % m], 1),
+                       seconds / 2, 5, 100000)
+    torch_all, torch_one, torch_n = _torch_cpu_us(sets[:max_sets], threads, seconds / 3)
+    med = statistics.median(many)
+    bytes_ = int4_bytes(N, K)
+    total_s = sum(many) + sum(one)
+    return {"value": round(bytes_ / med / 1e9, 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
-            "sample": f"20 calls (after 3 warmup) of the INT4 {N}x{K} GEMV "
-                      f"on one input set, median {med * 1e6:.1f} us; fused "
-                      f"unpack-dequant-dot in C + OpenMP",
+            "sample": f"{len(many)} calls of the INT4 {N}x{K} GEMV ({sum(many):.1f} s "
+                      f"of CPU work on {threads} threads), cycling over {m} distinct "
+                      f"host-resident input sets of the bench pool "
+                      f"({m * bytes_ / 1e6:.0f} MB), after 3 warm-up calls; median "
+                      f"{med * 1e6:.1f} us per call; fused unpack-dequant-dot in "
+                      f"C + OpenMP (oracle/qgemv_oracle.c)",
             "us_per_call": round(med * 1e6, 2),
-            "c_port_1_thread_us": round(one, 1),
+            "c_port_1_thread_us": round(statistics.median(one) * 1e6, 1),
+            "c_port_1_thread_calls": len(one),
+            "sample_cpu_seconds": round(total_s, 2),
             "torch_formulation_us": {"threads": threads, "all_threads": round(torch_all, 1),
                                      "one_thread": round(torch_one, 1),
+                                     "calls": torch_n,
                                      "what": "dequantize_w(W_packed, scale) then "
                                              "torch.mv(Wd, x.float()).half() on the CPU "
                                              "(cudalab/int4gemv_correctness.py:220-221), "
-                                             "median of 5 calls after 1 warmup"},
+                                             "cycling over the same sets, median per call "
+                                             "after 1 warm-up call"},
             "host": _host_cpu()}
 
 
-def _median_us(fn, n: int) -> float:
-    fn()
-    ts = []
-    for _ in range(n):
-        t0 = time.perf_counter()
-        fn()
-        ts.append(time.perf_counter() - t0)
-    return statistics.median(ts) * 1e6
-
-
-def _torch_cpu_us(wp, s, x, threads: int) -> tuple[float, float]:
-    """The reference's CPU path (dequantize then an FP32 torch.mv) with
-    `threads` threads and with one."""
+def _torch_cpu_us(sets, threads: int, seconds: float) -> tuple[float, float, list[int]]:
+    """The reference's CPU path (dequantize then an FP32 torch.mv) over
+    host copies of `sets`, with `threads` threads and with one: median us
+    per call and the call counts."""
     import torch
     from cudalab_amd.int4gemv_quantize import dequantize_w
+    host = [(wp.cpu(), s.cpu(), x.cpu()) for (wp, s, x, _) in sets]
 
-    def call():
+    def call(i):
+        wp, s, x = host[i % len(host)]
         torch.mv(dequantize_w(wp, s), x.float()).half()
     prev = torch.get_num_threads()
+    out = []
     try:
-        torch.set_num_threads(threads)
-        many = _median_us(call, 5)
-        torch.set_num_threads(1)
-        single = _median_us(call, 5)
+        for t in (threads, 1):
+            torch.set_num_threads(t)
+            call(0)
+            out.append(_timed_calls(call, seconds, 3, 10000))
     finally:
         torch.set_num_threads(prev)
-    return many, single
+    return (statistics.median(out[0]) * 1e6, statistics.median(out[1]) * 1e6,
+            [len(out[0]), len(out[1])])
 
 
 def _host_cpu() -> dict:
@@ -301,8 +327,7 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
-        cpu_sets, _ = make_sets("int4gemv", N, K, "hot")
-        cpu = cpu_baseline(N, K, cpu_sets)
+        cpu = cpu_baseline(N, K, sets, seconds=args.cpu_seconds)
 
     line = {
         "metric": METRIC,

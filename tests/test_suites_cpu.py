@@ -88,3 +88,28 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "8"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_bench_cpu_baseline_bounded_sample():
+    """bench.py's CPU leg on a tiny sample: the oracle port cycles over
+    distinct sets, reports medians and call counts, and its first result is
+    checked against the fp64 bound before anything is timed."""
+    import importlib.util
+    import torch
+    from cudalab_amd.int4gemv_quantize import quantize_w
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    g = torch.Generator().manual_seed(5)
+    sets = []
+    for _ in range(4):
+        W = (torch.randn(64, 256, generator=g) * 0.02).half()
+        wp, s = quantize_w(W)
+        sets.append((wp, s, torch.randn(256, generator=g).half(), None))
+    cpu = bench.cpu_baseline(64, 256, sets, seconds=0.05, max_sets=3)
+    assert cpu["kind"] == "port" and cpu["unit"] == "GB/s" and cpu["value"] > 0
+    assert cpu["cores"] >= 1 and cpu["us_per_call"] > 0
+    assert "cycling over 3 distinct host-resident input sets" in cpu["sample"]
+    assert cpu["c_port_1_thread_calls"] >= 5 and cpu["sample_cpu_seconds"] > 0
+    t = cpu["torch_formulation_us"]
+    assert min(t["calls"]) >= 3 and t["all_threads"] > 0 and t["one_thread"] > 0
