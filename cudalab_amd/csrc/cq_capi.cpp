@@ -54,6 +54,7 @@ constexpr Variant kVariants[] = {
     {"int4gemv_lds_r1", CQ_OP_INT4GEMV, cq::kLds, 1, false},
     {"int4gemv_lds_r2", CQ_OP_INT4GEMV, cq::kLds, 2, false},
     {"int4gemv_lds_r4", CQ_OP_INT4GEMV, cq::kLds, 4, false},
+    {"int4gemv_lds_tiled", CQ_OP_INT4GEMV, cq::kTiled, 0, false},
     {"qgemv_baseline", CQ_OP_QGEMV, cq::kScalar, 0, false},
     {"qgemv_cdna4", CQ_OP_QGEMV, cq::kLds, 0, false},
     {"qgemv_wave_r1", CQ_OP_QGEMV, cq::kWave, 1, false},
@@ -62,6 +63,7 @@ constexpr Variant kVariants[] = {
     {"qgemv_lds_r1", CQ_OP_QGEMV, cq::kLds, 1, false},
     {"qgemv_lds_r2", CQ_OP_QGEMV, cq::kLds, 2, false},
     {"qgemv_lds_r4", CQ_OP_QGEMV, cq::kLds, 4, false},
+    {"qgemv_lds_tiled", CQ_OP_QGEMV, cq::kTiled, 0, false},
     // gemv: one registry for both dtypes (listed under CQ_OP_GEMV_F16).
     // gemv_splitk4 keeps the reference's quarantined name for callers that
     // name it explicitly (kernels/gemv/bindings.cpp:50-80); it runs the
@@ -687,7 +689,12 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
     char line[512];
     std::snprintf(line, sizeof line,
                   "variant=%s kernel=%s cw=%d j=%d r=%d block=%d grid=%lld fallback=%d why=%s",
-                  v->name, p.kind == cq::kScalar ? "scalar" : (p.kind == cq::kLds ? "lds" : "wave"), p.cw, p.j, p.r,
+                  v->name,
+                  p.kind == cq::kScalar ? "scalar"
+                  : p.kind == cq::kLds  ? "lds"
+                  : p.kind == cq::kTiled ? "tiled"
+                                         : "wave",
+                  p.cw, p.j, p.r,
                   p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
                   p.why.empty() ? "-" : p.why.c_str());
     return write_out(line, buf, cap);

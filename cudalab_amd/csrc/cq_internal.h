@@ -11,12 +11,15 @@ namespace cq {
 
 // Kernel families.  kScalar is the single scalar source shared by the
 // *_baseline variants and by every fallback, so a fallback is bit-identical
-// to the baseline on the same input.  kWave is the CDNA4 wave64 kernel.
-enum Kind : int { kScalar = 0, kWave = 1, kLds = 2 };
+// to the baseline on the same input.  kWave is the CDNA4 wave64 kernel with
+// x in registers, kLds the one that stages x once per workgroup in LDS, and
+// kTiled the LDS kernel for rows of any length: one row per wave, x staged
+// tile by tile.
+enum Kind : int { kScalar = 0, kWave = 1, kLds = 2, kTiled = 3 };
 
-// Largest reduction length (elements) the wave kernels take; beyond it the
-// scalar kernel runs.  16384 = 8 register-resident x chunks per lane (INT4)
-// or 16 (INT8).
+// Largest reduction length (elements) the wave and LDS kernels take: 16384
+// = 8 chunks per lane (INT4) or 16 (INT8) held at once.  Beyond it the LDS
+// variants run the tiled kernel and the wave variants the scalar kernel.
 constexpr int64_t kMaxWaveK = 16384;
 
 // A resolved launch: which kernel instance and with what shape.

@@ -594,6 +594,230 @@ __global__ __launch_bounds__(NT) void qgemv_lds_kernel(
                               xcd_contiguous_block(), xs);
 }
 
+// K-tiled LDS kernels, for rows longer than one batch of chunks held per
+// lane (k > 16384; the *_lds_tiled variants force them at any k).  R rows
+// per wave (CW = 64), both read against one copy of x.  x is staged tile by
+// tile: TJ * 64 chunks of the row per tile (16384 INT4 or 8192 INT8
+// elements), re-paired in LDS, with a barrier before the tile is read and
+// one before the next tile overwrites it.  Every thread of the workgroup
+// runs the same tiles (they depend on nchunks only; rows past n are
+// clamped, never skipped), so every barrier is reached by all.  In the last,
+// partial tile only the first ceil(tc / 64) chunks of each lane are loaded
+// and summed (a wave-uniform bound).  Lane `col` takes chunks col + 64 j of
+// its rows in j order, as the untiled kernels do, so each row's sum
+// accumulates in the same order as an untiled kernel with J =
+// ceil(nchunks / 64): at k <= 16384 the result is bit-identical to the LDS
+// kernel with CW = 64 (for any R).
+template <int NT, int TJ, int R>
+__global__ __launch_bounds__(NT) void int4gemv_tiled_kernel(
+        const uint4* __restrict__ w, const uint16_t* __restrict__ scale,
+        const uint4* __restrict__ x, uint16_t* __restrict__ y, int n,
+        int nchunks) {
+    extern __shared__ uint4 xs[];                  // [4][TC + 1]
+    constexpr int TC = TJ * 64;                    // chunks per tile
+    constexpr int XPER = 4 * TC / NT;              // x pieces per thread per tile
+    static_assert(4 * TC % NT == 0, "a tile's pieces divide over the workgroup");
+    constexpr int ldsw = TC + 1;
+    const int tid = threadIdx.x;
+    const int col = tid & 63;
+    const int64_t row0 = (static_cast<int64_t>(xcd_contiguous_block()) * (NT >> 6) + (tid >> 6)) * R;
+    // Byte offsets within a row fit in 32 bits (the host checks
+    // n * k / 2 < 2^32); row bases are 64-bit.
+    const char* wrow[R];
+    const char* srow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint64_t rc = static_cast<uint64_t>(std::min<int64_t>(row0 + r, n - 1));
+        wrow[r] = reinterpret_cast<const char*>(w) + rc * (static_cast<uint32_t>(nchunks) * 16u);
+        srow[r] = reinterpret_cast<const char*>(scale) + rc * ((static_cast<uint32_t>(nchunks) >> 2) * 2u);
+    }
+    const f16x2 bias_lo = {static_cast<_Float16>(-1032.0f),
+                           static_cast<_Float16>(-1032.0f)};
+    const f16x2 bias_hi = {static_cast<_Float16>(-72.0f),
+                           static_cast<_Float16>(-72.0f)};
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    auto tile = [&]<bool PARTIAL>(int c0, int tc) {
+        const int jn = PARTIAL ? (tc + 63) >> 6 : TJ;   // chunks per lane, wave-uniform
+        const int np = 4 * tc;                          // x pieces in this tile
+        const uint4* xt = x + 4 * static_cast<int64_t>(c0);
+        uint4 xv[XPER];
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) xv[i] = xt[std::min(tid + i * NT, np - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        // this lane's chunks of the tile; lanes past the row end re-read the
+        // tile's last chunk against the zero column of x
+        uint4 wv[R][TJ];
+        uint16_t sv[R][TJ];
+        int xcol[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            if (PARTIAL && j >= jn) break;
+            const int c = col + 64 * j;
+            const uint32_t cl = static_cast<uint32_t>(c0 + (c < tc ? c : tc - 1));
+            xcol[j] = c < tc ? c : TC;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                wv[r][j] = *reinterpret_cast<const uint4*>(wrow[r] + cl * 16u);
+                sv[r][j] = *reinterpret_cast<const uint16_t*>(srow[r] + (cl >> 2) * 2u);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) {
+            const int p = std::min(tid + i * NT, np - 1);
+            const uint4 v = xv[i];
+            uint4 o;
+            o.x = (v.x & 0xFFFFu) | (v.z << 16);
+            o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+            o.z = (v.y & 0xFFFFu) | (v.w << 16);
+            o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+            xs[(p & 3) * ldsw + (p >> 2)] = o;
+        }
+        if (tid < 4) xs[tid * ldsw + TC] = uint4{0, 0, 0, 0};
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            if (PARTIAL && j >= jn) break;
+            float d[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) d[r] = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 xq = xs[q * ldsw + xcol[j]];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t u = q == 0 ? wv[r][j].x : q == 1 ? wv[r][j].y
+                                     : q == 2 ? wv[r][j].z : wv[r][j].w;
+                    const uint32_t u8 = u >> 8;
+                    const f16x2 qa = as_f16x2((u & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
+                    const f16x2 qb = as_f16x2((u & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
+                    const f16x2 qc = as_f16x2((u8 & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
+                    const f16x2 qd = as_f16x2((u8 & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
+                    d[r] = __builtin_amdgcn_fdot2(qa, as_f16x2(xq.x), d[r], false);
+                    d[r] = __builtin_amdgcn_fdot2(qb, as_f16x2(xq.y), d[r], false);
+                    d[r] = __builtin_amdgcn_fdot2(qc, as_f16x2(xq.z), d[r], false);
+                    d[r] = __builtin_amdgcn_fdot2(qd, as_f16x2(xq.w), d[r], false);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = __builtin_fmaf(h2f(sv[r][j]), d[r], acc[r]);
+        }
+        __syncthreads();
+    };
+    int c0 = 0;
+    for (; c0 + TC <= nchunks; c0 += TC) tile.template operator()<false>(c0, TC);
+    if (c0 < nchunks) tile.template operator()<true>(c0, nchunks - c0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float a = segment_sum<64>(acc[r]);
+        if (col == 63 && row0 + r < n) y[row0 + r] = f2h(a);
+    }
+}
+
+template <int NT, int TJ, int R>
+__global__ __launch_bounds__(NT) void qgemv_tiled_kernel(
+        const uint4* __restrict__ w, const float* __restrict__ scale,
+        const uint4* __restrict__ x, uint16_t* __restrict__ y, int n,
+        int nchunks) {
+    extern __shared__ uint4 xs[];                  // [2][TC + 1]
+    constexpr int TC = TJ * 64;
+    constexpr int XPER = 2 * TC / NT;
+    static_assert(2 * TC % NT == 0, "a tile's pieces divide over the workgroup");
+    constexpr int ldsw = TC + 1;
+    const int tid = threadIdx.x;
+    const int col = tid & 63;
+    const int64_t row0 = (static_cast<int64_t>(xcd_contiguous_block()) * (NT >> 6) + (tid >> 6)) * R;
+    const char* wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint64_t rc = static_cast<uint64_t>(std::min<int64_t>(row0 + r, n - 1));
+        wrow[r] = reinterpret_cast<const char*>(w) + rc * (static_cast<uint32_t>(nchunks) * 16u);
+    }
+    const f16x2 bias = {static_cast<_Float16>(-1152.0f),
+                        static_cast<_Float16>(-1152.0f)};
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    auto tile = [&]<bool PARTIAL>(int c0, int tc) {
+        const int jn = PARTIAL ? (tc + 63) >> 6 : TJ;
+        const int np = 2 * tc;
+        const uint4* xt = x + 2 * static_cast<int64_t>(c0);
+        uint4 xv[XPER];
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) xv[i] = xt[std::min(tid + i * NT, np - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        uint4 wv[R][TJ];
+        int xcol[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            if (PARTIAL && j >= jn) break;
+            const int c = col + 64 * j;
+            const uint32_t cl = static_cast<uint32_t>(c0 + (c < tc ? c : tc - 1));
+            xcol[j] = c < tc ? c : TC;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wv[r][j] = *reinterpret_cast<const uint4*>(wrow[r] + cl * 16u);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) {
+            const int p = std::min(tid + i * NT, np - 1);
+            const uint4 v = xv[i];
+            uint4 o;
+            o.x = (v.x & 0xFFFFu) | (v.y << 16);
+            o.y = (v.x >> 16) | (v.y & 0xFFFF0000u);
+            o.z = (v.z & 0xFFFFu) | (v.w << 16);
+            o.w = (v.z >> 16) | (v.w & 0xFFFF0000u);
+            xs[(p & 1) * ldsw + (p >> 1)] = o;
+        }
+        if (tid < 2) xs[tid * ldsw + TC] = uint4{0, 0, 0, 0};
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            if (PARTIAL && j >= jn) break;
+            const uint4 x0 = xs[xcol[j]];
+            const uint4 x1 = xs[ldsw + xcol[j]];
+            const uint32_t xpair[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t u = words[q];
+                    const f16x2 qp = as_f16x2((u & 0x00FF00FFu) ^ 0x64806480u) + bias;
+                    const f16x2 qq = as_f16x2(((u >> 8) & 0x00FF00FFu) ^ 0x64806480u) + bias;
+                    acc[r] = __builtin_amdgcn_fdot2(qp, as_f16x2(xpair[2 * q]), acc[r], false);
+                    acc[r] = __builtin_amdgcn_fdot2(qq, as_f16x2(xpair[2 * q + 1]), acc[r], false);
+                }
+            }
+        }
+        __syncthreads();
+    };
+    int c0 = 0;
+    for (; c0 + TC <= nchunks; c0 += TC) tile.template operator()<false>(c0, TC);
+    if (c0 < nchunks) tile.template operator()<true>(c0, nchunks - c0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float a = segment_sum<64>(acc[r]);
+        const int64_t row = row0 + r;
+        if (col == 63 && row < n) y[row] = f2h(scale[row] * a);
+    }
+}
+
+// Tile size of the K-tiled kernels (chunks per lane per tile), by rows per
+// wave.  Measured on MI355X over HBM-cold pools (k = 28672 .. 65536, n =
+// 1024 .. 16384): two rows per wave do best with 4 chunks per lane per
+// tile (INT4 8192x28672: 24.4 us against 29.3 us with one row and 8), one
+// row per wave with 8; 256-thread workgroups throughout.
+constexpr int tile_j(int r) { return r == 2 ? 4 : 8; }
+// LDS bytes of one tile: `pieces` 16-byte x pieces per chunk (INT4 4, INT8
+// 2), plus the zero column.
+constexpr uint32_t tile_lds(int pieces, int r) {
+    return static_cast<uint32_t>(pieces) * (tile_j(r) * 64 + 1) * 16u;
+}
+
 // Several independent problems of one k per launch (grouped GEMV).  The
 // problem table travels by value in the kernel arguments; logical
 // workgroups [start[p], start[p+1]) belong to problem p, and each computes
@@ -981,6 +1205,21 @@ Plan scalar_plan(int64_t n, bool fallback, const char* why) {
     return p;
 }
 
+// The K-tiled kernel: `rows` rows per wave if requested (1 or 2), else two
+// from n = 2048 on (the grid then still has a 256-thread workgroup for
+// every CU) and one below.
+Plan tiled_plan(int rows, int64_t n, int64_t nchunks) {
+    Plan p;
+    p.kind = kTiled;
+    p.cw = 64;
+    p.j = static_cast<int>((nchunks + 63) / 64);
+    p.r = rows > 0 ? std::min(rows, 2) : (n >= 2048 ? 2 : 1);
+    p.block = kBlock;
+    const int64_t waves = (n + p.r - 1) / p.r;
+    p.grid = (waves + kBlock / 64 - 1) / (kBlock / 64);
+    return p;
+}
+
 }  // namespace
 
 bool int4_contract_ok(const void* w, const void* x, int64_t k) {
@@ -995,15 +1234,17 @@ bool q8_contract_ok(const void* w, const void* x, int64_t k) {
            (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
+
 Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
                const void* x) {
     if (kind == kScalar) return scalar_plan(n, false, "");
     if (!int4_contract_ok(w, x, k))
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%32)");
-    if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
-    const int64_t nchunks = k / 32;
-    if (kind == kLds && n * (k / 2) >= (int64_t{1} << 32))
+    if ((kind == kLds || kind == kTiled) && n * (k / 2) >= (int64_t{1} << 32))
         return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
+    const int64_t nchunks = k / 32;
+    if (kind == kTiled || (kind == kLds && k > kMaxWaveK)) return tiled_plan(rows, n, nchunks);
+    if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
     p.cw = pow2_at_least(nchunks, 16);
@@ -1020,10 +1261,11 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
     if (kind == kScalar) return scalar_plan(n, false, "");
     if (!q8_contract_ok(w, x, k))
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%16)");
-    if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
-    const int64_t nchunks = k / 16;
-    if (kind == kLds && n * k >= (int64_t{1} << 32))
+    if ((kind == kLds || kind == kTiled) && n * k >= (int64_t{1} << 32))
         return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
+    const int64_t nchunks = k / 16;
+    if (kind == kTiled || (kind == kLds && k > kMaxWaveK)) return tiled_plan(rows, n, nchunks);
+    if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
     p.cw = pow2_at_least(nchunks, 16);
@@ -1044,6 +1286,14 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
                       static_cast<const uint16_t*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
+    if (p.kind == kTiled)
+        return launch(p.r == 2 ? int4gemv_tiled_kernel<kBlock, tile_j(2), 2>
+                               : int4gemv_tiled_kernel<kBlock, tile_j(1), 1>,
+                      p.grid, kBlock, tile_lds(4, p.r), stream, ev0, ev1,
+                      static_cast<const uint4*>(w),
+                      static_cast<const uint16_t*>(scale),
+                      static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
+                      static_cast<int>(n), static_cast<int>(k / 32));
     const Int4Fn fn =
         p.kind == kWave ? instance<Int4Wave>(p.cw, p.j, p.r)
         : p.block == 512 ? instance<Int4Lds<512>>(p.cw, p.j, p.r)
@@ -1066,6 +1316,13 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                       static_cast<const float*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
+    if (p.kind == kTiled)
+        return launch(p.r == 2 ? qgemv_tiled_kernel<kBlock, tile_j(2), 2>
+                               : qgemv_tiled_kernel<kBlock, tile_j(1), 1>,
+                      p.grid, kBlock, tile_lds(2, p.r), stream, ev0, ev1,
+                      static_cast<const uint4*>(w), static_cast<const float*>(scale),
+                      static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
+                      static_cast<int>(n), static_cast<int>(k / 16));
     const Q8Fn fn = p.kind == kWave ? instance<Q8Wave>(p.cw, p.j, p.r)
                     : p.block == 512 ? instance<Q8Lds<512>>(p.cw, p.j, p.r)
                                      : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);

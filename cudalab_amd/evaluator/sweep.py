@@ -63,44 +63,50 @@ def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
     return r["total_us"] / steps
 
 
+def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
+            steps: int, warmup: int) -> dict:
+    sets, nbytes = make_sets(op, N, K, mode)
+    x0 = sets[0][1] if op == "gemv" else sets[0][2]
+    plan = ext.describe(variant, sets[0][0], x0)
+    us = window_us(op, variant, sets, steps, warmup)
+    rec = {"op": op, "variant": variant, "N": N, "K": K, "mode": mode,
+           "pool_sets": len(sets), "bytes_per_call": nbytes,
+           "us_per_call": round(us, 4), "GBps": round(nbytes / us / 1e3, 1),
+           "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+           "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r", "block", "grid")}}
+    if mode == "streaming":
+        c = read_ceiling(nbytes, warmup=warmup, n_launches=steps)
+        rec["ceiling_us"] = round(c["us_per_call"], 4)
+        rec["frac_ceiling"] = round(c["us_per_call"] / us, 4)
+    del sets
+    torch.cuda.empty_cache()
+    return rec
+
+
 def run(ops=tuple(OPS), shapes=SHAPES, modes=("streaming", "hot"),
-        steps: int = 2000, warmup: int = 200) -> list[dict]:
+        steps: int = 2000, warmup: int = 200,
+        variants: dict | None = None) -> list[dict]:
+    """One record per (op, variant, shape, mode); `variants` maps an op to
+    the variants to time (default: its incumbent)."""
     out = []
     for op in ops:
         ext = build(op)
-        variant = OPS[op]
-        for (N, K) in shapes:
-            for mode in modes:
-                sets, nbytes = make_sets(op, N, K, mode)
-                x0 = sets[0][1] if op == "gemv" else sets[0][2]
-                plan = ext.describe(variant, sets[0][0], x0)
-                us = window_us(op, variant, sets, steps, warmup)
-                rec = {"op": op, "variant": variant, "N": N, "K": K,
-                       "mode": mode, "pool_sets": len(sets),
-                       "bytes_per_call": nbytes, "us_per_call": round(us, 4),
-                       "GBps": round(nbytes / us / 1e3, 1),
-                       "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-                       "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r",
-                                                      "block", "grid")}}
-                if mode == "streaming":
-                    c = read_ceiling(nbytes, warmup=warmup, n_launches=steps)
-                    rec["ceiling_us"] = round(c["us_per_call"], 4)
-                    rec["frac_ceiling"] = round(c["us_per_call"] / us, 4)
-                out.append(rec)
-                del sets
-                torch.cuda.empty_cache()
+        for variant in (variants or {}).get(op, [OPS[op]]):
+            for (N, K) in shapes:
+                for mode in modes:
+                    out.append(_record(op, ext, variant, N, K, mode, steps, warmup))
     return out
 
 
 def table(records: list[dict]) -> str:
-    lines = [f"{'op':<9} {'N':>6} {'K':>6} {'mode':<9} {'us/call':>8} "
+    lines = [f"{'variant':<20} {'N':>6} {'K':>6} {'mode':<9} {'us/call':>8} "
              f"{'GB/s':>7} {'%peak':>6} {'ceil_us':>8} {'%ceil':>6}  plan"]
     for r in records:
         p = r["plan"]
         plan = f"{p['kernel']} cw={p['cw']} j={p['j']} r={p['r']} block={p['block']} grid={p['grid']}"
         ceil = (f"{r['ceiling_us']:>8.3f} {100 * r['frac_ceiling']:>5.1f}%"
                 if "ceiling_us" in r else f"{'-':>8} {'-':>6}")
-        lines.append(f"{r['op']:<9} {r['N']:>6} {r['K']:>6} {r['mode']:<9} "
+        lines.append(f"{r['variant']:<20} {r['N']:>6} {r['K']:>6} {r['mode']:<9} "
                      f"{r['us_per_call']:>8.3f} {r['GBps']:>7.0f} "
                      f"{100 * r['frac_peak']:>5.1f}% {ceil}  {plan}")
     return "\n".join(lines)
@@ -108,7 +114,8 @@ def table(records: list[dict]) -> str:
 
 def speedups(records: list[dict]) -> str:
     """INT4 vs INT8 vs FP16 per shape and mode (µs ratios)."""
-    by = {(r["op"], r["N"], r["K"], r["mode"]): r["us_per_call"] for r in records}
+    by = {(r["op"], r["N"], r["K"], r["mode"]): r["us_per_call"] for r in records
+          if r["variant"] == OPS[r["op"]]}
     lines = [f"{'N':>6} {'K':>6} {'mode':<9} {'int4 us':>8} {'int8 us':>8} "
              f"{'fp16 us':>8} {'int8/int4':>9} {'fp16/int4':>9}"]
     for (op, N, K, mode), us in by.items():
@@ -128,15 +135,37 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--ops", default=",".join(OPS))
     ap.add_argument("--json", default=None)
+    ap.add_argument("--shapes", default=None,
+                    help='N x K list, e.g. "8192x28672,4096x4096" (default: the '
+                         "five bench shapes)")
+    ap.add_argument("--modes", default="streaming,hot")
+    ap.add_argument("--variant", action="append", default=[], metavar="OP=V1,V2",
+                    help="variants to time for an op (default: its incumbent)")
     a = ap.parse_args(argv)
     ops = tuple(o for o in a.ops.split(",") if o)
     if not ops or any(o not in OPS for o in ops):
         print(f"sweep: --ops must name some of {tuple(OPS)}", file=sys.stderr)
         return 2
+    try:
+        shapes = (SHAPES if a.shapes is None else
+                  [tuple(int(v) for v in s.lower().split("x")) for s in a.shapes.split(",") if s])
+        variants = {}
+        for spec in a.variant:
+            op, vs = spec.split("=", 1)
+            variants[op] = [v for v in vs.split(",") if v]
+    except ValueError:
+        print("sweep: --shapes takes NxK,NxK... and --variant OP=V1,V2", file=sys.stderr)
+        return 2
+    modes = tuple(m for m in a.modes.split(",") if m)
+    if (any(len(sh) != 2 for sh in shapes) or any(m not in ("streaming", "hot") for m in modes)
+            or any(op not in OPS for op in variants)):
+        print("sweep: bad --shapes, --modes or --variant", file=sys.stderr)
+        return 2
     if not torch.cuda.is_available():
         print("sweep: no GPU visible", file=sys.stderr)
         return 1
-    recs = run(ops=ops, steps=a.steps, warmup=a.warmup)
+    recs = run(ops=ops, shapes=shapes, modes=modes, steps=a.steps, warmup=a.warmup,
+               variants=variants)
     print(table(recs), flush=True)
     print("\n" + speedups(recs), flush=True)
     if a.json:

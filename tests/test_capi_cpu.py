@@ -98,8 +98,9 @@ def test_int4_launch_plans(n, k, kernel, cw, j, r, block):
 def test_int4_plans_fall_back_to_scalar():
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", 8, 4096, 4097, 8192)
     assert d["kernel"] == "scalar" and d["fallback"] == "1" and "alignment" in d["why"]
-    d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", 8, 16512, 4096, 8192)
-    assert d["kernel"] == "scalar" and d["fallback"] == "1"
+    # the wave variants hold x in registers: beyond 16384 they fall back
+    d = _capi.describe_launch("int4gemv", "int4gemv_wave_r1", 8, 16512, 4096, 8192)
+    assert d["kernel"] == "scalar" and d["fallback"] == "1" and "k above" in d["why"]
     d = _capi.describe_launch("int4gemv", "int4gemv_baseline", 8, 4096, 4096, 8192)
     assert d["kernel"] == "scalar" and d["fallback"] == "0"
     d = _capi.describe_launch("int4gemv", "int4gemv_rowtile4_hx", 8, 4096, 4096, 8192)
@@ -107,6 +108,41 @@ def test_int4_plans_fall_back_to_scalar():
     # weights of 4 GiB or more would overflow the 32-bit offsets
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", 1 << 20, 8192, 4096, 8192)
     assert d["kernel"] == "scalar" and "4 GiB" in d["why"]
+
+
+@pytest.mark.parametrize("op,variant,n,k,j,r", [
+    # k above 16384: the LDS variants run the K-tiled kernel on 256-thread
+    # workgroups, two rows per wave from n = 2048 on, one below
+    ("int4gemv", "int4gemv_cdna4", 8, 16512, 9, 1),
+    ("int4gemv", "int4gemv_cdna4", 8192, 28672, 14, 2),
+    ("int4gemv", "int4gemv_cdna4", 2047, 28672, 14, 1),
+    ("int4gemv", "int4gemv_lds_r2", 100, 20480, 10, 2),     # rows requested
+    ("int4gemv", "int4gemv_lds_r1", 8192, 20480, 10, 1),
+    ("int4gemv", "int4gemv_cdna4", 2048, 65536, 32, 2),
+    ("qgemv", "qgemv_cdna4", 8192, 28672, 28, 2),
+    ("qgemv", "qgemv_cdna4", 3, 16400, 17, 1),
+    # the *_lds_tiled variants force it at any k
+    ("int4gemv", "int4gemv_lds_tiled", 4096, 4096, 2, 2),
+    ("int4gemv", "int4gemv_lds_tiled", 1, 128, 1, 1),
+    ("qgemv", "qgemv_lds_tiled", 4097, 11008, 11, 2),
+])
+def test_tiled_plans(op, variant, n, k, j, r):
+    d = _capi.describe_launch(op, variant, n, k, 4096, 8192)
+    assert d["kernel"] == "tiled" and d["fallback"] == "0"
+    assert (int(d["cw"]), int(d["j"]), int(d["r"]), int(d["block"])) == (64, j, r, 256)
+    assert int(d["grid"]) == -(-(-(-n // r)) // 4)
+
+
+def test_tiled_keeps_the_fallbacks():
+    """The tiled kernel has the same vector contract and 32-bit offsets."""
+    d = _capi.describe_launch("int4gemv", "int4gemv_lds_tiled", 8, 4096, 4098, 8192)
+    assert d["kernel"] == "scalar" and "alignment" in d["why"]
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 8, 16392, 4096, 8192)   # k % 16
+    assert d["kernel"] == "scalar" and "k%16" in d["why"]
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 1 << 14, 1 << 18, 4096, 8192)
+    assert d["kernel"] == "scalar" and "4 GiB" in d["why"]
+    d = _capi.describe_launch("qgemv", "qgemv_wave_r1", 8, 16400, 4096, 8192)
+    assert d["kernel"] == "scalar" and "k above" in d["why"]
 
 
 def test_q8_launch_plans():
