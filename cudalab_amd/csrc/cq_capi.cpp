@@ -71,6 +71,7 @@ constexpr Variant kVariants[] = {
     // which is what the reference quarantined it for.
     {"gemv_baseline", CQ_OP_GEMV_F16, cq::kScalar, 0, false},
     {"gemv_cdna4", CQ_OP_GEMV_F16, cq::kLds, 0, false},
+    {"gemv_lds_tiled", CQ_OP_GEMV_F16, cq::kTiled, 0, false},
     {"gemv_splitk4", CQ_OP_GEMV_F16, cq::kScalar, 0, true},
 };
 

@@ -1008,6 +1008,81 @@ __global__ __launch_bounds__(NT) void gemv_lds_kernel(
     if (col == CW - 1 && row < n) fp_store(y + row, acc);
 }
 
+// K-tiled FP16/FP32 GEMV, for rows whose x does not fit the 64 KiB stage
+// (k > 32768 fp16, > 16384 fp32; gemv_lds_tiled forces it at any k).  64
+// lanes per row, one row per wave.  x is staged tile by tile (kGemvTileJ
+// chunks per lane per tile, 32 KB), with a barrier before the tile is read
+// and one before the next tile overwrites it; every thread runs the same
+// tiles (they depend on nchunks only; rows past n are clamped), so every
+// barrier is reached by all.  Within a tile the lane's W chunks stream
+// through two register batches of kGemvBatch chunks as in gemv_lds_kernel.
+// Lane `col` takes chunks col + 64 j in j order, so where x fits one stage
+// the sums are bit-identical to gemv_lds_kernel with CW = 64.
+constexpr int kGemvTileJ = 4 * kGemvBatch;    // 32 chunks per lane per tile
+constexpr uint32_t kGemvTileLds = (kGemvTileJ * 64 + 1) * 16u;   // 32,784 B
+
+template <typename S, int NT>
+__global__ __launch_bounds__(NT) void gemv_tiled_kernel(
+        const uint4* __restrict__ w,   // [n][nchunks] 16-byte chunks
+        const uint4* __restrict__ x,   // [nchunks] 16-byte chunks
+        S* __restrict__ y, int n, int nchunks) {
+    extern __shared__ uint4 xs[];                 // [TC + 1], the last zero
+    constexpr int JB = kGemvBatch;
+    constexpr int TC = kGemvTileJ * 64;           // chunks per tile
+    constexpr int XPER = TC / NT;                 // x chunks per thread per tile
+    static_assert(TC % NT == 0, "a tile's chunks divide over the workgroup");
+    const int tid = threadIdx.x;
+    const int col = tid & 63;
+    const int64_t row = static_cast<int64_t>(xcd_contiguous_block()) * (NT >> 6) + (tid >> 6);
+    const uint64_t rowc = static_cast<uint64_t>(std::min<int64_t>(row, n - 1));
+    const char* wrow = reinterpret_cast<const char*>(w) +
+                       rowc * (static_cast<uint32_t>(nchunks) * 16u);
+    float accs[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nchunks; c0 += TC) {
+        const int tc = std::min(TC, nchunks - c0);            // chunks in this tile
+        const int nbatch = ((tc + 63) / 64 + JB - 1) / JB;    // wave-uniform
+        const uint4* xt = x + c0;
+        uint4 xv[XPER];
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) xv[i] = xt[std::min(tid + i * NT, tc - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        uint4 wa[JB], wn[JB];
+        auto load = [&](uint4 (&dst)[JB], int b) {
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj) {
+                const int c = col + 64 * (b * JB + jj);
+                const uint32_t cl = static_cast<uint32_t>(c0 + (c < tc ? c : tc - 1));
+                dst[jj] = *reinterpret_cast<const uint4*>(wrow + cl * 16u);
+            }
+        };
+        load(wa, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < XPER; ++i) xs[std::min(tid + i * NT, tc - 1)] = xv[i];
+        if (tid == 0) xs[TC] = uint4{0, 0, 0, 0};
+        __syncthreads();
+        auto comp = [&](const uint4 (&src)[JB], int b) {
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj) {
+                const int c = col + 64 * (b * JB + jj);
+                dot_chunk(S{}, src[jj], xs[c < tc ? c : TC], accs);
+            }
+        };
+        for (int b = 0; b < nbatch; b += 2) {
+            if (b + 1 < nbatch) load(wn, b + 1);
+            comp(wa, b);
+            if (b + 1 < nbatch) {
+                if (b + 2 < nbatch) load(wa, b + 2);
+                comp(wn, b + 1);
+            }
+        }
+        __syncthreads();
+    }
+    float acc = (accs[0] + accs[1]) + (accs[2] + accs[3]);
+    acc = segment_sum<64>(acc);
+    if (col == 63 && row < n) fp_store(y + row, acc);
+}
+
 // ------------------------------------------------- read-only ceiling
 //
 // A plain streaming read of `bytes`, one 16-byte load per thread.  Of the
@@ -1469,11 +1544,19 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k % elements per 16 B)");
     const int64_t es = dtype == kF32 ? 4 : 2;
     const int64_t nchunks = k * es / 16;
-    if ((nchunks + 1) * 16 > kGemvMaxLdsBytes)
-        return scalar_plan(n, true, "x above the 64 KiB LDS staging limit");
     if (n * k * es >= (int64_t{1} << 32))
         return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
     Plan p;
+    if (kind == kTiled || (nchunks + 1) * 16 > kGemvMaxLdsBytes) {
+        // x staged tile by tile: 64 lanes per row, one row per wave
+        p.kind = kTiled;
+        p.cw = 64;
+        p.j = static_cast<int>((nchunks + 63) / 64);
+        p.r = 1;
+        p.block = (n + 7) / 8 >= kCus ? 512 : kBlock;
+        p.grid = (n + p.block / 64 - 1) / (p.block / 64);
+        return p;
+    }
     p.kind = kLds;
     p.cw = pow2_at_least(nchunks, 16);
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
@@ -1521,9 +1604,14 @@ hipError_t launch_gemv_t(const Plan& p, const void* w, const void* x, void* y,
         return launch(gemv_scalar_kernel<S>, p.grid, p.block, 0, stream, ev0,
                       ev1, static_cast<const S*>(w), static_cast<const S*>(x),
                       static_cast<S*>(y), k);
+    const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
+    if (p.kind == kTiled)
+        return launch(p.block == 512 ? gemv_tiled_kernel<S, 512> : gemv_tiled_kernel<S, kBlock>,
+                      p.grid, p.block, kGemvTileLds, stream, ev0, ev1,
+                      static_cast<const uint4*>(w), static_cast<const uint4*>(x),
+                      static_cast<S*>(y), static_cast<int>(n), nchunks);
     const GemvFn<S> fn = gemv_instance<S>(p.cw, p.j, p.block);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
     return launch(fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),
                   stream, ev0, ev1, static_cast<const uint4*>(w),
                   static_cast<const uint4*>(x), static_cast<S*>(y),

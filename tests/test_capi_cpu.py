@@ -295,17 +295,30 @@ def test_grouped_overlap_check_scales_and_allows_shared_inputs(monkeypatch):
     ("gemv_f32", 11008, 4096, "lds", 64, 16, 512),
     ("gemv_f16", 1024, 4096, "lds", 64, 8, 256),   # 512 would leave CUs idle
     ("gemv_f16", 7, 64, "lds", 16, 1, 256),
-    ("gemv_f32", 4096, 16384, "scalar", 0, 0, 0),    # x above the LDS limit
+    # x above the 64 KiB stage: the K-tiled kernel, one row per wave
+    ("gemv_f32", 4096, 16384, "tiled", 64, 64, 512),
+    ("gemv_f16", 8192, 65536, "tiled", 64, 128, 512),
+    ("gemv_f16", 300, 40000, "tiled", 64, 79, 256),
+    ("gemv_f16", 4096, 32760, "lds", 64, 64, 512),   # the largest x that fits
     ("gemv_f16", 16, 13, "scalar", 0, 0, 0),         # K % 8 != 0
 ])
 def test_gemv_launch_plans(op, n, k, kernel, cw, j, block):
     d = _capi.describe_launch(op, "gemv_cdna4", n, k, 4096, 8192)
     assert (d["kernel"], int(d["cw"]), int(d["j"])) == (kernel, cw, j)
-    if kernel == "lds":
+    if kernel in ("lds", "tiled"):
         assert d["fallback"] == "0" and int(d["block"]) == block
         assert int(d["grid"]) == -(-n // ((64 // cw) * (block // 64)))
     else:
         assert d["fallback"] == "1"
+
+
+def test_gemv_tiled_variant_plans():
+    d = _capi.describe_launch("gemv_f16", "gemv_lds_tiled", 4096, 4096, 4096, 8192)
+    assert (d["kernel"], d["cw"], d["r"], d["block"]) == ("tiled", "64", "1", "512")
+    d = _capi.describe_launch("gemv_f32", "gemv_lds_tiled", 5, 20, 4096, 8192)   # k % 4
+    assert d["kernel"] == "tiled" and d["block"] == "256" and d["grid"] == "2"
+    d = _capi.describe_launch("gemv_f16", "gemv_lds_tiled", 5, 20, 4096, 8192)   # k % 8
+    assert d["kernel"] == "scalar" and d["fallback"] == "1"
 
 
 def test_gemv_argument_errors_without_launch():

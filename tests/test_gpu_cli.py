@@ -83,7 +83,8 @@ def test_regression_gemv(cuda, tmp_path, capsys):
     assert audit["gemv"]["quarantined_variants()"] == ["gemv_splitk4"]
     assert "gemv_splitk4" not in audit["gemv"]["variants()"]
     summary = json.loads((tmp_path / "summary.json").read_text())
-    assert set(summary["gemv"]["variants_run"]) == {"gemv_baseline", "gemv_cdna4"}
+    assert set(summary["gemv"]["variants_run"]) == {"gemv_baseline", "gemv_cdna4",
+                                                    "gemv_lds_tiled"}
 
 
 def test_gen3_native_timing(cuda, tmp_path, capsys):

@@ -21,12 +21,12 @@ BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
 # (3, 16376): the largest fp16 K whose x fits the 64 KiB LDS stage is 32760;
 # (5, 16380) fp32 uses exactly 64 KiB; (2, 32768) fp16 is past the limit and
-# takes the scalar kernel; (4099, 4096) has a partial last workgroup.
+# takes the K-tiled kernel; (4099, 4096) has a partial last workgroup.
 # (4099, 4096), (4097, 1024), (4097, 11008): partial last workgroups of the
 # 512-thread plans, with register batches of 8, 2 and 8 (three batches) chunks
 EXTRA = [(3, 16376), (5, 16380), (2, 32768), (4099, 4096), (33, 1000),
          (17, 24), (4097, 1024), (4097, 11008)]
-VARIANTS = ("gemv_baseline", "gemv_cdna4", "gemv_splitk4")
+VARIANTS = ("gemv_baseline", "gemv_cdna4", "gemv_lds_tiled", "gemv_splitk4")
 
 
 @pytest.fixture(scope="module")
@@ -46,7 +46,7 @@ def _np(t):
 
 
 def test_registry(extg):
-    assert extg.variants() == ["gemv_baseline", "gemv_cdna4"]
+    assert extg.variants() == ["gemv_baseline", "gemv_cdna4", "gemv_lds_tiled"]
     assert extg.quarantined_variants() == ["gemv_splitk4"]
     assert extg.aliases() == {"gemv_vec4_row": "gemv_cdna4",
                               "gemv_warp_vec4": "gemv_cdna4"}

@@ -35,14 +35,16 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def _check_bound(y, ex, S, K, what):
-    """Rows whose exact value fits fp16 pass the bound; rows clearly past
-    the fp16 range (|exact| >= 65520, where round-to-nearest gives inf, with
-    a margin for the accumulation error) are inf of the right sign."""
+def _check_bound(y, ex, S, K, what, ratio=None):
+    """Rows whose exact value fits fp16 pass the bound (`ratio`, default the
+    INT4/INT8 one); rows clearly past the fp16 range (|exact| >= 65520,
+    where round-to-nearest gives inf, with a margin for the accumulation
+    error) are inf of the right sign."""
+    ratio = ratio or orc.arith_ratio
     yn = _np(y).astype(np.float64)
     fits = np.abs(ex) <= 65504.0
     over = np.abs(ex) >= 65520.0 * (1 + 1e-3)
-    r = orc.arith_ratio(_np(y)[fits], ex[fits], S[fits], K)
+    r = ratio(_np(y)[fits], ex[fits], S[fits], K)
     assert np.all(np.isfinite(yn[fits])) and (r.size == 0 or r.max() <= 1.0), \
         (what, float(r.max()) if r.size else None)
     assert np.all(np.isinf(yn[over]) & (np.sign(yn[over]) == np.sign(ex[over]))), what
@@ -142,3 +144,61 @@ def test_large_k_grouped_and_side_stream(ext4, ext8):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     assert torch.equal(y, ref)
+
+
+# FP16/FP32 GEMV: x above the 64 KiB LDS stage (k > 32760 fp16, > 16380
+# fp32) runs the K-tiled kernel; gemv_lds_tiled forces it at any k.
+GEMV_LARGE_K = [(torch.float16, 2, 32768), (torch.float16, 300, 40000),
+                (torch.float16, 33, 65536), (torch.float32, 64, 20000),
+                (torch.float32, 5, 16388)]
+# shapes at which gemv_cdna4 runs 64 lanes per row (more than 32 chunks)
+GEMV_SAME_ORDER = [(torch.float16, 4096, 4096), (torch.float16, 300, 16376),
+                   (torch.float16, 33, 1000), (torch.float16, 4097, 11008),
+                   (torch.float32, 4096, 4096), (torch.float32, 77, 16380)]
+
+
+@pytest.fixture(scope="module")
+def extg(cuda):
+    from cudalab_amd.build import build
+    return build("gemv")
+
+
+def _gemv(N, K, dtype, mode, seed):
+    from cudalab_amd.operators.gemv import make_w, make_x
+    return (make_w(N, K, dtype, seed=seed, mode=mode, large=10.0),
+            make_x(K, dtype, seed=seed + 1, mode=mode, large=10.0))
+
+
+@pytest.mark.parametrize("dtype,N,K", GEMV_LARGE_K,
+                         ids=[f"{str(d)[-7:]}-{n}x{k}" for d, n, k in GEMV_LARGE_K])
+def test_gemv_large_k_bound(extg, dtype, N, K):
+    for mode in MODES:
+        W, x = _gemv(N, K, dtype, mode, seed=5)
+        if mode == "normal":
+            assert extg.describe("gemv_cdna4", W, x)["kernel"] == "tiled"
+        ex, S = orc.exact_gemv(_np(W), _np(x))
+        for v in ("gemv_cdna4", "gemv_lds_tiled", "gemv_baseline"):
+            announce(f"gemv tiled bound {v} {dtype} N={N} K={K} mode={mode}")
+            y = extg.forward(v, W, x)
+            torch.cuda.synchronize()
+            yn = _np(y)
+            if dtype == torch.float16:
+                _check_bound(y, ex, S, K, (v, mode),
+                             ratio=lambda a, e, s_, k: orc.arith_ratio_gemv(a, e, s_, k, np.float16))
+            else:
+                r = orc.arith_ratio_gemv(yn, ex, S, K, yn.dtype)
+                assert np.all(np.isfinite(yn)) and r.max() <= 1.0, (v, mode, float(r.max()))
+
+
+@pytest.mark.parametrize("dtype,N,K", GEMV_SAME_ORDER,
+                         ids=[f"{str(d)[-7:]}-{n}x{k}" for d, n, k in GEMV_SAME_ORDER])
+def test_gemv_tiled_matches_untiled_lane_order(extg, dtype, N, K):
+    for mode in ("normal", "large", "mixed_sign"):
+        W, x = _gemv(N, K, dtype, mode, seed=6)
+        d = extg.describe("gemv_cdna4", W, x)
+        assert (d["kernel"], d["cw"]) == ("lds", "64")
+        announce(f"gemv tiled == cdna4 {dtype} N={N} K={K} mode={mode}")
+        a = extg.forward("gemv_lds_tiled", W, x)
+        b = extg.forward("gemv_cdna4", W, x)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (dtype, N, K, mode)

@@ -184,8 +184,9 @@ def test_gemv_cases_in_reference_order(eg, monkeypatch):
 
 
 def test_gemv_registry(eg):
-    assert eg.variants() == ["gemv_baseline", "gemv_cdna4"]
+    assert eg.variants() == ["gemv_baseline", "gemv_cdna4", "gemv_lds_tiled"]
     assert eg.quarantined_variants() == ["gemv_splitk4"]
-    assert eg.all_variants() == ["gemv_baseline", "gemv_cdna4", "gemv_splitk4"]
+    assert eg.all_variants() == ["gemv_baseline", "gemv_cdna4", "gemv_lds_tiled",
+                                 "gemv_splitk4"]
     assert eg.resolve("gemv_vec4_row") == "gemv_cdna4"
     assert eg.resolve("gemv_warp_vec4") == "gemv_cdna4"
