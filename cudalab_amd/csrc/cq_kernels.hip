@@ -1315,10 +1315,12 @@ Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
     if (kind == kScalar) return scalar_plan(n, false, "");
     if (!int4_contract_ok(w, x, k))
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%32)");
-    if ((kind == kLds || kind == kTiled) && n * (k / 2) >= (int64_t{1} << 32))
-        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
     const int64_t nchunks = k / 32;
-    if (kind == kTiled || (kind == kLds && k > kMaxWaveK)) return tiled_plan(rows, n, nchunks);
+    // the untiled LDS kernels address W with 32-bit byte offsets; the tiled
+    // kernel keeps 64-bit row bases, so it also takes weights of 4 GiB or more
+    const bool big = n * (k / 2) >= (int64_t{1} << 32);
+    if (kind == kTiled || (kind == kLds && (k > kMaxWaveK || big)))
+        return tiled_plan(rows, n, nchunks);
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
@@ -1336,10 +1338,10 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
     if (kind == kScalar) return scalar_plan(n, false, "");
     if (!q8_contract_ok(w, x, k))
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k%16)");
-    if ((kind == kLds || kind == kTiled) && n * k >= (int64_t{1} << 32))
-        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
     const int64_t nchunks = k / 16;
-    if (kind == kTiled || (kind == kLds && k > kMaxWaveK)) return tiled_plan(rows, n, nchunks);
+    const bool big = n * k >= (int64_t{1} << 32);    // as in plan_int4
+    if (kind == kTiled || (kind == kLds && (k > kMaxWaveK || big)))
+        return tiled_plan(rows, n, nchunks);
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
@@ -1544,10 +1546,14 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
         return scalar_plan(n, true, "vector contract unmet (w/x 16B alignment, k % elements per 16 B)");
     const int64_t es = dtype == kF32 ? 4 : 2;
     const int64_t nchunks = k * es / 16;
-    if (n * k * es >= (int64_t{1} << 32))
-        return scalar_plan(n, true, "weights of 4 GiB or more (32-bit offsets)");
+    // in-row byte offsets are 32-bit in every vector kernel; row bases are
+    // 64-bit only in the tiled kernel, which therefore also takes weights
+    // of 4 GiB or more
+    if (k * es >= (int64_t{1} << 32))
+        return scalar_plan(n, true, "rows of 4 GiB or more (32-bit offsets)");
+    const bool big = n * k * es >= (int64_t{1} << 32);
     Plan p;
-    if (kind == kTiled || (nchunks + 1) * 16 > kGemvMaxLdsBytes) {
+    if (kind == kTiled || big || (nchunks + 1) * 16 > kGemvMaxLdsBytes) {
         // x staged tile by tile: 64 lanes per row, one row per wave
         p.kind = kTiled;
         p.cw = 64;

@@ -105,9 +105,12 @@ def test_int4_plans_fall_back_to_scalar():
     assert d["kernel"] == "scalar" and d["fallback"] == "0"
     d = _capi.describe_launch("int4gemv", "int4gemv_rowtile4_hx", 8, 4096, 4096, 8192)
     assert d["variant"] == "int4gemv_cdna4" and d["kernel"] == "lds"
-    # weights of 4 GiB or more would overflow the 32-bit offsets
+    # weights of 4 GiB or more would overflow the untiled kernels' 32-bit
+    # offsets: the tiled kernel (64-bit row bases) takes them
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", 1 << 20, 8192, 4096, 8192)
-    assert d["kernel"] == "scalar" and "4 GiB" in d["why"]
+    assert d["kernel"] == "tiled" and d["fallback"] == "0"
+    d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", (1 << 20) - 1, 8192, 4096, 8192)
+    assert d["kernel"] == "lds"
 
 
 @pytest.mark.parametrize("op,variant,n,k,j,r", [
@@ -140,7 +143,13 @@ def test_tiled_keeps_the_fallbacks():
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 8, 16392, 4096, 8192)   # k % 16
     assert d["kernel"] == "scalar" and "k%16" in d["why"]
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 1 << 14, 1 << 18, 4096, 8192)
-    assert d["kernel"] == "scalar" and "4 GiB" in d["why"]
+    assert d["kernel"] == "tiled"                       # 4 GiB of weights
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 1 << 18, 1 << 14, 4096, 8192)
+    assert d["kernel"] == "tiled" and d["r"] == "2"     # 4 GiB, short rows
+    d = _capi.describe_launch("gemv_f16", "gemv_cdna4", 1 << 17, 1 << 14, 4096, 8192)
+    assert d["kernel"] == "tiled"                       # 4 GiB of fp16 weights
+    d = _capi.describe_launch("gemv_f32", "gemv_cdna4", 2, 1 << 30, 4096, 8192)
+    assert d["kernel"] == "scalar" and "rows of 4 GiB" in d["why"]
     d = _capi.describe_launch("qgemv", "qgemv_wave_r1", 8, 16400, 4096, 8192)
     assert d["kernel"] == "scalar" and "k above" in d["why"]
 

@@ -202,3 +202,55 @@ def test_gemv_tiled_matches_untiled_lane_order(extg, dtype, N, K):
         b = extg.forward("gemv_cdna4", W, x)
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (dtype, N, K, mode)
+
+
+@pytest.mark.parametrize("op", ["int4gemv", "qgemv", "gemv"])
+def test_weights_of_4gib_or_more(op, ext4, ext8, extg):
+    """W of just over 4 GiB with short rows (k = 8192): the untiled kernels'
+    32-bit offsets cannot reach it, so the incumbents plan the tiled kernel
+    (64-bit row bases).  Rows on both sides of the 4 GiB byte mark, and the
+    first and last rows, are checked against the oracle (sampled rows only:
+    the whole matrix is not copied to the host)."""
+    K = 8192
+    row_bytes = {"int4gemv": K // 2, "qgemv": K, "gemv": 2 * K}[op]
+    first_past = (1 << 32) // row_bytes          # first row starting at or past 4 GiB
+    N = first_past + 3
+    g = torch.Generator(device="cuda").manual_seed(11)
+    announce(f"{op} weights of 4 GiB or more: N={N} K={K}")
+    x = torch.randn(K, device="cuda", generator=g).half()
+    rows = torch.tensor([0, 1, N // 2, first_past - 2, first_past - 1, first_past,
+                         first_past + 1, N - 1], device="cuda")
+    if op == "int4gemv":
+        W = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device="cuda", generator=g)
+        s = (torch.rand(N, K // 128, device="cuda", generator=g) * 1e-2 + 1e-3).half()
+        ext, args = ext4, (W, s, x)
+        assert ext.describe("int4gemv_cdna4", W, x)["kernel"] == "tiled"
+        ex, S = orc.exact_w4(_np(W[rows]), _np(s[rows]), _np(x))
+        ratio = orc.arith_ratio
+        variants = ("int4gemv_cdna4", "int4gemv_baseline")
+    elif op == "qgemv":
+        W = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+        s = torch.rand(N, device="cuda", generator=g) * 1e-2 + 1e-3
+        ext, args = ext8, (W, s, x)
+        assert ext.describe("qgemv_cdna4", W, x)["kernel"] == "tiled"
+        ex, S = orc.exact_w8(_np(W[rows]), _np(s[rows]), _np(x))
+        ratio = orc.arith_ratio
+        variants = ("qgemv_cdna4", "qgemv_baseline")
+    else:
+        W = (torch.randn(N, K, device="cuda", generator=g, dtype=torch.float16) * 0.02)
+        ext, args = extg, (W, x)
+        assert ext.describe("gemv_cdna4", W, x)["kernel"] == "tiled"
+        ex, S = orc.exact_gemv(_np(W[rows]), _np(x))
+        ratio = lambda a, e, s_, k: orc.arith_ratio_gemv(a, e, s_, k, np.float16)  # noqa: E731
+        variants = ("gemv_cdna4", "gemv_baseline")
+    assert W.numel() * W.element_size() > (1 << 32)
+    for v in variants:
+        announce(f"{op} 4 GiB weights {v}")
+        y = ext.forward(v, *args)
+        torch.cuda.synchronize()
+        yr = _np(y[rows])
+        assert np.all(np.isfinite(yr)), v
+        r = ratio(yr, ex, S, K)
+        assert r.max() <= 1.0, (v, float(r.max()))
+    del W, args
+    torch.cuda.empty_cache()
