@@ -1,18 +1,24 @@
 """Decode-step driver: the seven weight projections of every layer of a
-Llama-7B-shaped model, back to back on one GPU, through the INT4 (or INT8)
-GEMV path.  No counterpart in the reference (it excludes model
+Llama-shaped model (7B or 70B), back to back on one GPU, through the INT4
+(or INT8) GEMV path.  No counterpart in the reference (it excludes model
 integration: README.md:34-35); this restates the "back-to-back Llama-7B
 decode projections" workload of the benchmark configuration.
 
-Per layer, hidden H = 4096 and intermediate I = 11008:
-  q, k, v   H -> H   from the layer input       (independent: one group)
+Per layer, hidden H, intermediate I and k/v width KV (KV = H without
+grouped-query attention; Llama-70B: H = 8192, I = 28672, KV = 1024):
+  q         H -> H   from the layer input       (q, k, v independent:
+  k, v      H -> KV  from the layer input        one group)
   o         H -> H   from v                     (a single-token context makes
-                                                 attention the identity on v)
+                                                 attention the identity on v;
+                                                 with KV < H each kv head's v
+                                                 is repeated for its H/KV
+                                                 query heads, one small copy)
   gate, up  H -> I   from o                     (independent: one group)
   down      I -> H   from up                    (feeds the next layer)
 Norms, attention over a longer context, the residual adds and the SwiGLU
 product are outside the GEMV path and are not modelled; the data
-dependencies between projections follow the layer's order.
+dependencies between projections follow the layer's order.  At 70B the
+down projection (K = 28672) runs the K-tiled kernel.
 
 Weights are random-init: W ~ N(0, 1/K) in fp16 (so activations stay O(1)
 through all layers), quantized with the path's own quantizers on the
@@ -22,8 +28,9 @@ device.  Three ways to run one decode step over all layers:
   graph       the grouped step captured once in a HIP graph and replayed
 All three produce bit-identical outputs.
 
-Usage: python -m cudalab_amd.decode [--layers 32] [--op int4gemv]
-       [--steps 20] [--warmup 3] [--modes sequential,grouped,graph]
+Usage: python -m cudalab_amd.decode [--model 7b|70b] [--layers N]
+       [--op int4gemv|qgemv] [--steps 20] [--warmup 3]
+       [--modes sequential,grouped,graph]
 """
 from __future__ import annotations
 
@@ -39,10 +46,21 @@ from .build import build
 HIDDEN = 4096
 INTER = 11008
 LAYERS = 32
+HEAD_DIM = 128
+# Llama-shaped presets: hidden, intermediate, k/v width, layers
+MODELS = {"7b": dict(hidden=4096, inter=11008, kv=4096, layers=32),
+          "70b": dict(hidden=8192, inter=28672, kv=1024, layers=80)}
 VARIANT = {"int4gemv": "int4gemv_cdna4", "qgemv": "qgemv_cdna4"}
-PROJ = (("q", HIDDEN, HIDDEN), ("k", HIDDEN, HIDDEN), ("v", HIDDEN, HIDDEN),
-        ("o", HIDDEN, HIDDEN), ("gate", INTER, HIDDEN), ("up", INTER, HIDDEN),
-        ("down", HIDDEN, INTER))
+
+
+def projections(hidden: int, inter: int, kv: int):
+    """(name, N, K) of one layer's seven projections."""
+    return (("q", hidden, hidden), ("k", kv, hidden), ("v", kv, hidden),
+            ("o", hidden, hidden), ("gate", inter, hidden), ("up", inter, hidden),
+            ("down", hidden, inter))
+
+
+PROJ = projections(HIDDEN, INTER, HIDDEN)
 
 
 def _quantize(op: str, W: torch.Tensor):
@@ -73,14 +91,17 @@ class DecodeModel:
 
     def __init__(self, op: str = "int4gemv", layers: int = LAYERS,
                  seed: int = 7, device: str = "cuda",
-                 hidden: int = HIDDEN, inter: int = INTER):
+                 hidden: int = HIDDEN, inter: int = INTER,
+                 kv: int | None = None):
         self.op = op
         self.ext = build(op)
         self.variant = VARIANT[op]
-        self.hidden, self.inter = hidden, inter
-        self.proj = tuple((n, (hidden if a == HIDDEN else inter),
-                           (hidden if b == HIDDEN else inter))
-                          for (n, a, b) in PROJ)
+        kv = hidden if kv is None else kv
+        if hidden % kv or kv % HEAD_DIM:
+            raise ValueError(f"k/v width {kv} must divide hidden {hidden} and be a "
+                             f"multiple of the head size {HEAD_DIM}")
+        self.hidden, self.inter, self.kv = hidden, inter, kv
+        self.proj = projections(hidden, inter, kv)
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         self.layers: list[Layer] = []
@@ -92,6 +113,9 @@ class DecodeModel:
                 L.w[name] = _quantize(op, W)
                 L.out[name] = torch.empty(N, dtype=torch.float16, device=device)
                 del W
+            # o's input: v itself, or v repeated per query head group
+            L.out["o_in"] = (L.out["v"] if kv == hidden else
+                             torch.empty(hidden, dtype=torch.float16, device=device))
             self.layers.append(L)
         self.x0 = (torch.randn(hidden, generator=g, device=device)).half()
         self.bytes_per_step = layers * sum(proj_bytes(op, N, K)
@@ -106,12 +130,22 @@ class DecodeModel:
         self.ext.forward_grouped(self.variant, [(L.w[n][0], L.w[n][1], x, L.out[n])
                                                 for n in names])
 
+    def _attend(self, L: Layer) -> torch.Tensor:
+        """Attention over a single-token context: each query head gets its
+        kv head's v (a copy when k/v are narrower than the hidden size)."""
+        if self.kv == self.hidden:
+            return L.out["v"]
+        kvh, rep = self.kv // HEAD_DIM, self.hidden // self.kv
+        L.out["o_in"].view(kvh, rep, HEAD_DIM).copy_(
+            L.out["v"].view(kvh, 1, HEAD_DIM).expand(kvh, rep, HEAD_DIM))
+        return L.out["o_in"]
+
     def step_sequential(self) -> torch.Tensor:
         x = self.x0
         for L in self.layers:
             for n in ("q", "k", "v"):
                 self._one(L, n, x)
-            self._one(L, "o", L.out["v"])
+            self._one(L, "o", self._attend(L))
             for n in ("gate", "up"):
                 self._one(L, n, L.out["o"])
             self._one(L, "down", L.out["up"])
@@ -122,7 +156,7 @@ class DecodeModel:
         x = self.x0
         for L in self.layers:
             self._group(L, ("q", "k", "v"), x)
-            self._one(L, "o", L.out["v"])
+            self._one(L, "o", self._attend(L))
             self._group(L, ("gate", "up"), L.out["o"])
             self._one(L, "down", L.out["up"])
             x = L.out["down"]
@@ -142,6 +176,9 @@ class DecodeModel:
 
     def outputs(self) -> list[torch.Tensor]:
         return [L.out[n].clone() for L in self.layers for n, _, _ in self.proj]
+
+    def layer_bytes(self) -> int:
+        return self.bytes_per_step // len(self.layers)
 
 
 def time_steps(fn, steps: int, warmup: int) -> float:
@@ -163,11 +200,15 @@ def time_steps(fn, steps: int, warmup: int) -> float:
 MODES = ("sequential", "grouped", "graph")
 
 
-def run(op: str = "int4gemv", layers: int = LAYERS, steps: int = 20,
-        warmup: int = 3, modes=MODES) -> dict:
-    m = DecodeModel(op, layers)
+def run(op: str = "int4gemv", layers: int | None = None, steps: int = 20,
+        warmup: int = 3, modes=MODES, model: str = "7b") -> dict:
+    cfg = MODELS[model]
+    layers = cfg["layers"] if layers is None else layers
+    m = DecodeModel(op, layers, hidden=cfg["hidden"], inter=cfg["inter"],
+                    kv=cfg["kv"])
     graph = m.capture() if "graph" in modes else None
-    res = {"op": op, "variant": m.variant, "layers": layers,
+    res = {"op": op, "variant": m.variant, "model": model, "layers": layers,
+           "hidden": m.hidden, "inter": m.inter, "kv": m.kv,
            "bytes_per_step": m.bytes_per_step,
            "launches_per_layer": {"sequential": 7, "grouped": 4, "graph": 4},
            "note": "sequential and grouped include the Python API path of "
@@ -188,7 +229,9 @@ def run(op: str = "int4gemv", layers: int = LAYERS, steps: int = 20,
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--op", choices=tuple(VARIANT), default="int4gemv")
-    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--model", choices=tuple(MODELS), default="7b")
+    ap.add_argument("--layers", type=int, default=None,
+                    help="layers (default: the model's, 32 for 7b, 80 for 70b)")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--modes", default=",".join(MODES),
@@ -198,10 +241,13 @@ def main(argv=None) -> int:
     if not modes or any(m not in MODES for m in modes):
         print(f"decode: --modes must name some of {MODES}", file=sys.stderr)
         return 2
+    if a.layers is not None and a.layers < 1:
+        print("decode: --layers must be >= 1", file=sys.stderr)
+        return 2
     if not torch.cuda.is_available():
         print("decode: no GPU visible", file=sys.stderr)
         return 1
-    print(json.dumps(run(a.op, a.layers, a.steps, a.warmup, modes)), flush=True)
+    print(json.dumps(run(a.op, a.layers, a.steps, a.warmup, modes, a.model)), flush=True)
     return 0
 
 
