@@ -1234,10 +1234,15 @@ int pow2_at_least(int64_t v, int lo) {
 }
 
 // Default rows per lane (measured on MI355X, streaming and hot): INT4 takes
-// two rows per lane when that still leaves at least 2048 waves (8 per CU),
-// otherwise one; INT8 does best with one row per lane at every bench shape.
-int default_rows_int4(int64_t n, int slots, int rmax) {
+// two rows per lane when each lane holds at most 2 chunks of a row and that
+// still leaves at least 2048 waves (8 per CU), otherwise one; INT8 does best
+// with one row per lane at every bench shape.  With 4 chunks per lane (k =
+// 8192) one row is 10-13% faster than two (8192^2: 8.42 vs 9.36 us,
+// 28672x8192: 22.4 vs 25.9 us); with 2 the two are level (4096^2: 3.94 vs
+// 3.95 us).
+int default_rows_int4(int64_t n, int slots, int j, int rmax) {
     constexpr int64_t min_waves = 2048;
+    if (j > 2) return 1;
     const int r = std::min(2, rmax);
     const int64_t waves = (n + slots * r - 1) / (slots * r);
     return (r == 2 && waves >= min_waves) ? 2 : 1;
@@ -1327,7 +1332,7 @@ Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
     p.cw = pow2_at_least(nchunks, 16);
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
     const int rmax = int4_rmax(p.j);
-    p.r = rows > 0 ? std::min(rows, rmax) : default_rows_int4(n, 64 / p.cw, rmax);
+    p.r = rows > 0 ? std::min(rows, rmax) : default_rows_int4(n, 64 / p.cw, p.j, rmax);
     if (p.r == 3) p.r = 2;
     finish_wave_plan(p, n, true);
     return p;

@@ -86,6 +86,10 @@ def test_vector_contract_predicate():
     (5, 16384, "lds", 64, 8, 1, 256),
     # two rows per lane but fewer than 256 workgroups at 512 threads
     (3000, 4096, "lds", 64, 2, 1, 256),
+    # 4 chunks per lane (k = 8192): one row per lane at any n
+    (8192, 8192, "lds", 64, 4, 1, 512),
+    (57344, 8192, "lds", 64, 4, 1, 512),
+    (4096, 6144, "lds", 64, 3, 1, 512),
 ])
 def test_int4_launch_plans(n, k, kernel, cw, j, r, block):
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", n, k, 4096, 8192)
