@@ -1233,19 +1233,23 @@ int pow2_at_least(int64_t v, int lo) {
     return p;
 }
 
-// Default rows per lane (measured on MI355X, streaming and hot): INT4 takes
-// two rows per lane when each lane holds at most 2 chunks of a row and that
-// still leaves at least 2048 waves (8 per CU), otherwise one; INT8 does best
-// with one row per lane at every bench shape.  With 4 chunks per lane (k =
-// 8192) one row is 10-13% faster than two (8192^2: 8.42 vs 9.36 us,
-// 28672x8192: 22.4 vs 25.9 us); with 2 the two are level (4096^2: 3.94 vs
-// 3.95 us).
+// Default rows per lane (measured on MI355X, streaming, decided with the
+// paired A/B engine): INT4 takes two rows per lane only when each lane
+// holds at most 2 chunks of a row, that leaves at least 2048 waves, and
+// the 512-thread workgroups of that plan fill the CUs in whole rounds
+// (their count a multiple of kCus); otherwise one row on 256-thread
+// workgroups.  4096^2 (256 workgroups): two rows are faster (A/B CI95 of
+// one/two [0.917, 0.991]); 6144x4096 (384): one row is a KEEP at 1.10x;
+// 11008x4096 and 14336x4096: one row level or 0.5-1% faster; with 4
+// chunks per lane (k = 8192) one row is 11-15% faster.  INT8 does best
+// with one row per lane at every bench shape.
+constexpr int64_t kCus = 256;
 int default_rows_int4(int64_t n, int slots, int j, int rmax) {
     constexpr int64_t min_waves = 2048;
-    if (j > 2) return 1;
-    const int r = std::min(2, rmax);
-    const int64_t waves = (n + slots * r - 1) / (slots * r);
-    return (r == 2 && waves >= min_waves) ? 2 : 1;
+    if (j > 2 || rmax < 2) return 1;
+    const int64_t waves = (n + slots * 2 - 1) / (slots * 2);
+    const int64_t grid = (waves + 7) / 8;          // 512-thread workgroups
+    return (waves >= min_waves && grid % kCus == 0) ? 2 : 1;
 }
 
 // Workgroup size of the LDS kernels.  512 threads halve the number of
@@ -1255,7 +1259,6 @@ int default_rows_int4(int64_t n, int slots, int j, int rmax) {
 // per lane (4096^2: 3.82 -> 3.79 us) or with 3+ chunks per lane (4096x11008:
 // 7.44 -> 6.93 us), INT8 with 8+ chunks per lane (4096x11008: 10.48 ->
 // 9.88 us).  INT8 at K = 4096 was 1-3% slower with 512.
-constexpr int64_t kCus = 256;
 int lds_threads(bool int4, int r, int j, int64_t waves) {
     const bool fills = (waves + 7) / 8 >= kCus;
     if (int4 && (r == 2 || j >= 3) && fills) return 512;

@@ -77,14 +77,16 @@ def test_vector_contract_predicate():
 
 
 @pytest.mark.parametrize("n,k,kernel,cw,j,r,block", [
-    (4096, 4096, "lds", 64, 2, 2, 512),
-    (11008, 4096, "lds", 64, 2, 2, 512),
+    (4096, 4096, "lds", 64, 2, 2, 512),      # 256 workgroups: whole rounds
+    (8192, 4096, "lds", 64, 2, 2, 512),      # 512
+    (11008, 4096, "lds", 64, 2, 1, 256),     # 688 would leave a partial round
+    (6144, 4096, "lds", 64, 2, 1, 256),      # 384: one row is 1.10x faster
     (4096, 11008, "lds", 64, 6, 1, 512),      # 3+ chunks per lane: 512 threads
     (1024, 4096, "lds", 64, 2, 1, 256),
     (4096, 1024, "lds", 32, 1, 1, 256),
     (1, 128, "lds", 16, 1, 1, 256),
     (5, 16384, "lds", 64, 8, 1, 256),
-    # two rows per lane but fewer than 256 workgroups at 512 threads
+    # two rows per lane would leave fewer than 2048 waves
     (3000, 4096, "lds", 64, 2, 1, 256),
     # 4 chunks per lane (k = 8192): one row per lane at any n
     (8192, 8192, "lds", 64, 4, 1, 512),

@@ -17,10 +17,11 @@ MODES = ("normal", "zeros", "tiny", "large", "mixed_sign")
 EDGE = [(1, 128), (1, 4096), (3, 128), (16, 256), (8, 128)]
 BENCH = [(1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
          (4096, 11008)]
-# (4099, 4096): two rows per lane on 512-thread workgroups with a partial
-# last workgroup and a grid (257) that is not a multiple of the 8 XCDs
-# (4099, 4096) and (4097, 11008): partial last workgroups of the 512-thread
-# plans (two rows per lane; 3+ chunks per lane)
+# (4099, 4096): int4gemv_lds_r2 runs two rows per lane on 512-thread
+# workgroups with a partial last workgroup and a grid (257) that is not a
+# multiple of the 8 XCDs (the incumbent takes one row there: 257 workgroups
+# would leave a partial round); (4097, 11008): partial last workgroup of the
+# 512-thread plan with 3+ chunks per lane
 EXTRA = [(5, 16384), (7, 16512), (1, 2048), (65, 384), (300, 1280),
          (4099, 4096), (4097, 11008)]
 
