@@ -46,7 +46,12 @@
  * cq_last_error() returns a message for the calling thread.  Metadata
  * validation with the reference's messages (dtype, contiguity, device) is
  * the Python layer's job; this layer re-checks only what it needs to launch
- * safely (non-null pointers, positive sizes, k % 128 for int4gemv).
+ * safely (non-null pointers, positive sizes, k % 128 for int4gemv, outputs
+ * that share no byte with the inputs).
+ *
+ * Any k: rows longer than 16384 elements (int4gemv, qgemv) or whose x
+ * exceeds 64 KiB (gemv), and weights of 4 GiB or more, run K-tiled
+ * vectorized kernels on the LDS variants (describe reports kernel=tiled).
  */
 #ifndef CDNAQGEMV_H
 #define CDNAQGEMV_H
