@@ -1254,15 +1254,21 @@ int default_rows_int4(int64_t n, int slots, int j, int rmax) {
 
 // Workgroup size of the LDS kernels.  512 threads halve the number of
 // workgroups that stage x.  Measured on MI355X (same launch path, HBM-cold
-// pools) this pays as long as the grid still has a workgroup for every CU
-// (256) and x is large next to each workgroup's weights: INT4 with two rows
-// per lane (4096^2: 3.82 -> 3.79 us) or with 3+ chunks per lane (4096x11008:
-// 7.44 -> 6.93 us), INT8 with 8+ chunks per lane (4096x11008: 10.48 ->
-// 9.88 us).  INT8 at K = 4096 was 1-3% slower with 512.
+// pools) this pays when x is large next to each workgroup's weights (INT4
+// with two rows per lane or 3+ chunks per lane, INT8 with 8+ chunks per
+// lane: 4096x11008 INT4 7.44 -> 6.93 us, INT8 10.48 -> 9.88 us) and the
+// 512-thread grid fills the CUs in whole rounds (a multiple of kCus
+// workgroups) or runs many (8+) of them.  A partial round among few costs
+// more than the staging saves: 5120x13824 (640 workgroups of 512, 2.5
+// rounds; 1280 of 256) INT4 10.2 us with 512 threads, 9.8 with 256, INT8
+// 15.4 and 14.6; 5120^2 INT4 5.15 and 4.8.  Among many rounds the partial
+// one matters less: 27648x5120 (13.5 rounds) 15.8-16.0 us with 512, 16.0-16.3
+// with 256.  INT8 at K = 4096 was 1-3% slower with 512.
 int lds_threads(bool int4, int r, int j, int64_t waves) {
-    const bool fills = (waves + 7) / 8 >= kCus;
-    if (int4 && (r == 2 || j >= 3) && fills) return 512;
-    if (!int4 && j >= 8 && fills) return 512;
+    const int64_t grid = (waves + 7) / 8;
+    const bool rounds_ok = grid >= kCus && (grid % kCus == 0 || grid >= 8 * kCus);
+    if (int4 && (r == 2 || j >= 3) && rounds_ok) return 512;
+    if (!int4 && j >= 8 && rounds_ok) return 512;
     return kBlock;
 }
 

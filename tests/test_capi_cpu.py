@@ -92,6 +92,10 @@ def test_vector_contract_predicate():
     (8192, 8192, "lds", 64, 4, 1, 512),
     (57344, 8192, "lds", 64, 4, 1, 512),
     (4096, 6144, "lds", 64, 3, 1, 512),
+    # 512 threads only for whole rounds of 256 workgroups, or 8+ rounds
+    (5120, 5120, "lds", 64, 3, 1, 256),      # 640: 2.5 rounds
+    (5120, 13824, "lds", 64, 7, 1, 256),
+    (27648, 5120, "lds", 64, 3, 1, 512),     # 3456: 13.5 rounds
 ])
 def test_int4_launch_plans(n, k, kernel, cw, j, r, block):
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", n, k, 4096, 8192)
@@ -169,6 +173,9 @@ def test_q8_launch_plans():
     assert (d["j"], d["block"], d["grid"]) == ("11", "512", "512")
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 1024, 11008, 4096, 8192)
     assert (d["j"], d["block"], d["grid"]) == ("11", "256", "256")
+    # 640 workgroups of 512 would be 2.5 rounds over the CUs: 256 threads
+    d = _capi.describe_launch("qgemv", "qgemv_cdna4", 5120, 13824, 4096, 8192)
+    assert (d["j"], d["block"], d["grid"]) == ("14", "256", "1280")
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 16, 13, 4096, 8192)
     assert d["kernel"] == "scalar" and d["fallback"] == "1"
     d = _capi.describe_launch("qgemv", "qgemv_wave_r4", 64, 4096, 4096, 8192)
