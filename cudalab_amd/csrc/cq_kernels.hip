@@ -1264,9 +1264,15 @@ int default_rows_int4(int64_t n, int slots, int j, int rmax) {
 // 15.4 and 14.6; 5120^2 INT4 5.15 and 4.8.  Among many rounds the partial
 // one matters less: 27648x5120 (13.5 rounds) 15.8-16.0 us with 512, 16.0-16.3
 // with 256.  INT8 at K = 4096 was 1-3% slower with 512.
-int lds_threads(bool int4, int r, int j, int64_t waves) {
+// True when `waves` in 512-thread workgroups fill the CUs in whole rounds
+// or in 8+ rounds (the condition for 512-thread plans, all operators).
+bool rounds_ok_512(int64_t waves) {
     const int64_t grid = (waves + 7) / 8;
-    const bool rounds_ok = grid >= kCus && (grid % kCus == 0 || grid >= 8 * kCus);
+    return grid >= kCus && (grid % kCus == 0 || grid >= 8 * kCus);
+}
+
+int lds_threads(bool int4, int r, int j, int64_t waves) {
+    const bool rounds_ok = rounds_ok_512(waves);
     if (int4 && (r == 2 || j >= 3) && rounds_ok) return 512;
     if (!int4 && j >= 8 && rounds_ok) return 512;
     return kBlock;
@@ -1573,7 +1579,7 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
         p.cw = 64;
         p.j = static_cast<int>((nchunks + 63) / 64);
         p.r = 1;
-        p.block = (n + 7) / 8 >= kCus ? 512 : kBlock;
+        p.block = rounds_ok_512(n) ? 512 : kBlock;
         p.grid = (n + p.block / 64 - 1) / (p.block / 64);
         return p;
     }
@@ -1582,10 +1588,11 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
     p.j = static_cast<int>((nchunks + p.cw - 1) / p.cw);
     p.r = 1;
     const int64_t waves = (n + (64 / p.cw) - 1) / (64 / p.cw);
-    // 512-thread workgroups halve the x stagings; measured 16% faster at
-    // fp16 4096^2 and 3-4% at 4096x11008 / 11008x4096, when the grid still
-    // covers every CU
-    p.block = (waves + 7) / 8 >= kCus ? 512 : kBlock;
+    // 512-thread workgroups halve the x stagings: 16-20% faster at fp16
+    // 4096^2 and 15% at 6144x4096 (whole rounds of CUs); with a partial
+    // round among few (5120^2, 5120x13824: 2.5 rounds) 256 threads are 6-7%
+    // faster; among 5+ rounds the two are level
+    p.block = rounds_ok_512(waves) ? 512 : kBlock;
     p.grid = (waves + p.block / 64 - 1) / (p.block / 64);
     return p;
 }

@@ -314,7 +314,9 @@ def test_grouped_overlap_check_scales_and_allows_shared_inputs(monkeypatch):
     ("gemv_f16", 4096, 4096, "lds", 64, 8, 512),
     ("gemv_f32", 4096, 4096, "lds", 64, 16, 512),
     ("gemv_f16", 4096, 11008, "lds", 64, 22, 512),
-    ("gemv_f32", 11008, 4096, "lds", 64, 16, 512),
+    ("gemv_f32", 11008, 4096, "lds", 64, 16, 256),   # 1376 of 512: 5.4 rounds
+    ("gemv_f16", 6144, 4096, "lds", 64, 8, 512),     # 768 of 512: 3 whole rounds
+    ("gemv_f16", 5120, 13824, "lds", 64, 27, 256),   # 640 of 512: 2.5 rounds
     ("gemv_f16", 1024, 4096, "lds", 64, 8, 256),   # 512 would leave CUs idle
     ("gemv_f16", 7, 64, "lds", 16, 1, 256),
     # x above the 64 KiB stage: the K-tiled kernel, one row per wave
