@@ -9,6 +9,10 @@ events (cq_pool_timing), the same as bench.py's headline.  The read
 ceiling is cq_read_ceiling over an equally cold pool of the same bytes.
 
 Usage: python -m cudalab_amd.evaluator.sweep [--steps K] [--json FILE]
+           [--ops int4gemv,qgemv,gemv] [--modes streaming,hot]
+           [--shapes NxK,NxK...] [--variant OP=V1,V2 ...]
+Other shapes (e.g. Llama-70B's 8192x28672) and several variants per
+operator (e.g. the incumbent against *_lds_tiled) time the same way.
 """
 from __future__ import annotations
 

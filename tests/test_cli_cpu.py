@@ -118,3 +118,19 @@ def test_gen3_uses_the_reference_variant_names():
     assert gen3.GENERATIONS == (("gemv", "gemv_vec4_row"), ("qgemv", "qgemv_vec16_row"),
                                 ("int4gemv", "int4gemv_rowtile4_hx"))
     assert regression.OPS == ("int4gemv", "gemv", "qgemv")
+
+
+def test_sweep_options(monkeypatch, capsys):
+    """The sweep's --shapes / --modes / --variant options parse and reject
+    malformed values before touching a GPU."""
+    import torch
+    from cudalab_amd.evaluator import sweep
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert sweep.main(["--shapes", "8192x28672,4096x4096"]) == 1     # parsed, no GPU
+    assert sweep.main(["--variant", "int4gemv=int4gemv_cdna4,int4gemv_lds_tiled",
+                       "--modes", "streaming"]) == 1
+    for bad in (["--shapes", "8x8x8"], ["--shapes", "8xq"], ["--modes", "warm"],
+                ["--variant", "softmax=x"], ["--variant", "int4gemv"], ["--ops", "rmsnorm"]):
+        assert sweep.main(bad) == 2, bad
+    err = capsys.readouterr().err
+    assert "no GPU visible" in err and "--shapes" in err
