@@ -362,15 +362,28 @@ __global__ __launch_bounds__(kBlock) void qgemv_wave_kernel(
 // high nibble is taken in place (bits 4-7) under the fp16 exponent of 64,
 // where the mantissa step is 1/16, so ((w & 0x00F000F0) ^ 0x54805480) is
 // the fp16 pair (72+q1, 72+q5) and a packed add of -72 gives (q1, q5)
-// exactly.  Issue order: the workgroup's x pieces, then per row the weight
-// chunks and their group scales, so that each row's arithmetic waits only
-// for its own loads while later rows are still in flight.  Workgroups take
-// their rows through xcd_contiguous_block(); NT (256 or 512 threads) is
-// chosen by the host plan.
+// exactly.  Workgroups take their rows through xcd_contiguous_block(); NT
+// (256 or 512 threads) is chosen by the host plan.
+//
+// Address work is kept off the VALU, which these kernels are short of (the
+// INT4 dequant and dot take 13 VALU instructions per 8 weights):
+// - The host plans J = ceil(nchunks / CW), so a lane's chunks col + CW*j for
+//   j < J - 1 always lie inside the row; only the last one is clamped.
+//   The others sit at compile-time offsets from one per-lane address.
+// - The LDS planes have the compile-time stride CW*J + 1; column CW*J is
+//   zero and is what lanes past the row end read.  Every x read but the
+//   last chunk's is then an immediate offset from one address.
+// - The row base is wave-uniform when a row spans the wave (CW = 64), so it
+//   lives in scalar registers.
+// Issue order, pinned with scheduling barriers: the workgroup's x pieces,
+// then per row, chunk by chunk, the group scale and the weight chunk
+// (INT8: the chunks, then the row scale), so that the wait before chunk j
+// covers chunks 0..j only and each chunk is summed as it lands.  A
+// scheduling barrier after the workgroup barrier keeps weight arithmetic
+// (and its waits) from being hoisted above it.
 
 // The rows of logical workgroup `blk` of one INT4 problem.  `xs` is the
-// workgroup's LDS: [4][nchunks + 1] re-paired x pieces, q-major; column
-// nchunks is zero and is what lanes past the row end read.
+// workgroup's LDS: [4][CW*J + 1] re-paired x pieces, q-major.
 template <int CW, int J, int R, int NT>
 __device__ __forceinline__ void int4_lds_rows(
         const uint4* __restrict__ w,         // [n][nchunks] 16-byte chunks
@@ -379,53 +392,52 @@ __device__ __forceinline__ void int4_lds_rows(
         uint16_t* __restrict__ y, int n, int nchunks, uint32_t blk,
         uint4* __restrict__ xs) {
     constexpr int SLOTS = 64 / CW;
+    constexpr int S = CW * J + 1;                     // LDS plane stride
+    constexpr int XPER = (4 * CW * J + NT - 1) / NT;  // x pieces per thread
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int col = lane % CW;
     const int slot = lane / CW;
-    const uint32_t ngroups = static_cast<uint32_t>(nchunks) >> 2;
     const int npieces = 4 * nchunks;
-    const int ldsw = nchunks + 1;
-    const int64_t wave_id =
-        static_cast<int64_t>(blk) * (NT >> 6) + (tid >> 6);
+    const int64_t wave_id = static_cast<int64_t>(blk) * (NT >> 6) +
+                            __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
-    // Byte offsets fit in 32 bits (the host checks n * k / 2 < 2^32), so
-    // every load is one SGPR base plus one 32-bit VGPR offset.
+    // Byte offsets fit in 32 bits (the host checks n * k / 2 < 2^32).
     const char* wb = reinterpret_cast<const char*>(w);
     const char* sb = reinterpret_cast<const char*>(scale);
     const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
+    const uint32_t srow_bytes = static_cast<uint32_t>(nchunks >> 2) * 2u;
 
-    // (1) this thread's share of x first (npieces <= 256 * J <= NT * XPER)
-    constexpr int XPER = (256 * J + NT - 1) / NT;
+    // (1) this thread's share of x first
     uint4 xv[XPER];
 #pragma unroll
     for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * NT, npieces - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    // (2) weights and group scales, row by row, all in flight together;
-    //     lanes past the row end re-read the last chunk (x is zero there)
-    uint32_t woff[J], soff[J];
-    int xcol[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = col + CW * j;
-        const int cl = c < nchunks ? c : nchunks - 1;
-        xcol[j] = c < nchunks ? c : nchunks;
-        woff[j] = static_cast<uint32_t>(cl) * 16u;
-        soff[j] = static_cast<uint32_t>(cl >> 2) * 2u;
-    }
+    // (2) per row, each chunk's group scale and then the chunk, all in
+    //     flight together; a last chunk past the row end re-reads chunk
+    //     nchunks - 1 (x is zero there)
+    const int clast = col + CW * (J - 1);
+    const int cl = clast < nchunks ? clast : nchunks - 1;
+    const uint32_t wcol = static_cast<uint32_t>(col) * 16u;
+    const uint32_t scol = static_cast<uint32_t>(col >> 2) * 2u;
     uint4 wv[R][J];
     uint16_t sv[R][J];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t row = static_cast<uint32_t>(std::min<int64_t>(row0 + SLOTS * r, n - 1));
+        const char* wr = wb + row * wrow_bytes;
+        const char* sr = sb + row * srow_bytes;
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-            wv[r][j] = *reinterpret_cast<const uint4*>(wb + (row * wrow_bytes + woff[j]));
-#pragma unroll
-        for (int j = 0; j < J; ++j)
-            sv[r][j] = *reinterpret_cast<const uint16_t*>(sb + (row * ngroups * 2u + soff[j]));
+        for (int j = 0; j < J; ++j) {
+            const bool in_row = j < J - 1;
+            sv[r][j] = *reinterpret_cast<const uint16_t*>(
+                sr + (in_row ? scol + (CW / 2) * j : static_cast<uint32_t>(cl >> 2) * 2u));
+            __builtin_amdgcn_sched_barrier(0);
+            wv[r][j] = *reinterpret_cast<const uint4*>(
+                wr + (in_row ? wcol + CW * 16 * j : static_cast<uint32_t>(cl) * 16u));
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
-    __builtin_amdgcn_sched_barrier(0);
     // (3) re-pair x: piece = x0..x7 -> [(x0,x4), (x1,x5), (x2,x6), (x3,x7)]
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
@@ -439,15 +451,18 @@ __device__ __forceinline__ void int4_lds_rows(
         o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
         o.z = (v.y & 0xFFFFu) | (v.w << 16);
         o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-        xs[(p & 3) * ldsw + (p >> 2)] = o;
+        xs[(p & 3) * S + (p >> 2)] = o;
     }
-    if (tid < 4) xs[tid * ldsw + nchunks] = uint4{0, 0, 0, 0};
+    if (tid < 4) xs[tid * S + CW * J] = uint4{0, 0, 0, 0};
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     uint4 xp[J][4];
+    const int xlast = clast < nchunks ? clast : CW * J;
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xp[j][q] = xs[q * ldsw + xcol[j]];
+        for (int q = 0; q < 4; ++q)
+            xp[j][q] = xs[q * S + (j < J - 1 ? col + CW * j : xlast)];
 
     const f16x2 bias_lo = {static_cast<_Float16>(-1032.0f),
                            static_cast<_Float16>(-1032.0f)};
@@ -483,7 +498,9 @@ __device__ __forceinline__ void int4_lds_rows(
 }
 
 // The rows of logical workgroup `blk` of one INT8 problem; `xs` holds
-// [2][nchunks + 1] re-paired x pieces, q-major, column nchunks zero.
+// [2][CW*J + 1] re-paired x pieces, q-major, column CW*J zero.  Same
+// layout and issue order as the INT4 rows; the row's scale is loaded right
+// after its weights, so the final scaling waits on no load of its own.
 template <int CW, int J, int R, int NT>
 __device__ __forceinline__ void q8_lds_rows(
         const uint4* __restrict__ w,       // [n][nchunks] 16 int8 per chunk
@@ -492,15 +509,15 @@ __device__ __forceinline__ void q8_lds_rows(
         uint16_t* __restrict__ y, int n, int nchunks, uint32_t blk,
         uint4* __restrict__ xs) {
     constexpr int SLOTS = 64 / CW;
-    constexpr int XPER = (128 * J + NT - 1) / NT;   // x pieces per thread
+    constexpr int S = CW * J + 1;
+    constexpr int XPER = (2 * CW * J + NT - 1) / NT;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int col = lane % CW;
     const int slot = lane / CW;
     const int npieces = 2 * nchunks;
-    const int ldsw = nchunks + 1;
-    const int64_t wave_id =
-        static_cast<int64_t>(blk) * (NT >> 6) + (tid >> 6);
+    const int64_t wave_id = static_cast<int64_t>(blk) * (NT >> 6) +
+                            __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t row0 = wave_id * (SLOTS * R) + slot;
     const char* wb = reinterpret_cast<const char*>(w);
     const uint32_t wrow_bytes = static_cast<uint32_t>(nchunks) * 16u;
@@ -509,23 +526,25 @@ __device__ __forceinline__ void q8_lds_rows(
 #pragma unroll
     for (int i = 0; i < XPER; ++i) xv[i] = x[std::min(tid + i * NT, npieces - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t woff[J];
-    int xcol[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = col + CW * j;
-        xcol[j] = c < nchunks ? c : nchunks;
-        woff[j] = static_cast<uint32_t>(c < nchunks ? c : nchunks - 1) * 16u;
-    }
+    const int clast = col + CW * (J - 1);
+    const int cl = clast < nchunks ? clast : nchunks - 1;
+    const uint32_t wcol = static_cast<uint32_t>(col) * 16u;
     uint4 wv[R][J];
+    float sc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t row = static_cast<uint32_t>(std::min<int64_t>(row0 + SLOTS * r, n - 1));
+        const char* wr = wb + row * wrow_bytes;
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-            wv[r][j] = *reinterpret_cast<const uint4*>(wb + (row * wrow_bytes + woff[j]));
+        for (int j = 0; j < J; ++j) {
+            const uint32_t off = j < J - 1 ? wcol + CW * 16 * j
+                                           : static_cast<uint32_t>(cl) * 16u;
+            wv[r][j] = *reinterpret_cast<const uint4*>(wr + off);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        sc[r] = scale[row];
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
     // re-pair x: piece = x0..x7 -> [(x0,x2), (x1,x3), (x4,x6), (x5,x7)]
 #pragma unroll
     for (int i = 0; i < XPER; ++i) {
@@ -536,15 +555,18 @@ __device__ __forceinline__ void q8_lds_rows(
         o.y = (v.x >> 16) | (v.y & 0xFFFF0000u);
         o.z = (v.z & 0xFFFFu) | (v.w << 16);
         o.w = (v.z >> 16) | (v.w & 0xFFFF0000u);
-        xs[(p & 1) * ldsw + (p >> 1)] = o;
+        xs[(p & 1) * S + (p >> 1)] = o;
     }
-    if (tid < 2) xs[tid * ldsw + nchunks] = uint4{0, 0, 0, 0};
+    if (tid < 2) xs[tid * S + CW * J] = uint4{0, 0, 0, 0};
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     uint4 xp[J][2];
+    const int xlast = clast < nchunks ? clast : CW * J;
 #pragma unroll
     for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int q = 0; q < 2; ++q) xp[j][q] = xs[q * ldsw + xcol[j]];
+        for (int q = 0; q < 2; ++q)
+            xp[j][q] = xs[q * S + (j < J - 1 ? col + CW * j : xlast)];
 
     const f16x2 bias = {static_cast<_Float16>(-1152.0f),
                         static_cast<_Float16>(-1152.0f)};
@@ -569,8 +591,22 @@ __device__ __forceinline__ void q8_lds_rows(
         }
         acc = segment_sum<CW>(acc);
         const int64_t row = row0 + SLOTS * r;
-        if (col == CW - 1 && row < n) y[row] = f2h(scale[row] * acc);
+        if (col == CW - 1 && row < n) y[row] = f2h(sc[r] * acc);
     }
+}
+
+// LDS bytes of the untiled INT4 / INT8 LDS kernels for plan (cw, j).
+constexpr uint32_t int4_lds_bytes(int cw, int j) {
+    return 4u * 16u * static_cast<uint32_t>(cw * j + 1);
+}
+constexpr uint32_t q8_lds_bytes(int cw, int j) {
+    return 2u * 16u * static_cast<uint32_t>(cw * j + 1);
+}
+// The LDS kernels read chunks col + cw*j for j < J - 1 unclamped, which
+// stays inside a row only when J = ceil(nchunks / cw); every plan has that
+// form, and launches check it.
+inline bool lds_chunks_ok(const Plan& p, int64_t nchunks) {
+    return p.cw > 0 && p.j == (nchunks + p.cw - 1) / p.cw;
 }
 
 // One problem per launch.
@@ -1396,7 +1432,8 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
         : p.block == 512 ? instance<Int4Lds<512>>(p.cw, p.j, p.r)
                          : instance<Int4Lds<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 64) : 0;
+    if (p.kind == kLds && !lds_chunks_ok(p, k / 32)) return hipErrorInvalidConfiguration;
+    const uint32_t shmem = p.kind == kLds ? int4_lds_bytes(p.cw, p.j) : 0;
     return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
                   static_cast<const uint4*>(w),
                   static_cast<const uint16_t*>(scale),
@@ -1424,7 +1461,8 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                     : p.block == 512 ? instance<Q8Lds<512>>(p.cw, p.j, p.r)
                                      : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    const uint32_t shmem = p.kind == kLds ? static_cast<uint32_t>(2 * k + 32) : 0;
+    if (p.kind == kLds && !lds_chunks_ok(p, k / 16)) return hipErrorInvalidConfiguration;
+    const uint32_t shmem = p.kind == kLds ? q8_lds_bytes(p.cw, p.j) : 0;
     return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
                   static_cast<const uint4*>(w), static_cast<const float*>(scale),
                   static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
@@ -1531,7 +1569,8 @@ hipError_t launch_int4_group(const Plan& p, const GroupProblem* probs,
     const Int4GroupFn fn = p.block == 512
                                ? instance<Int4LdsGroup<512>>(p.cw, p.j, p.r)
                                : instance<Int4LdsGroup<kBlock>>(p.cw, p.j, p.r);
-    return launch_group(fn, p, g, grid, static_cast<uint32_t>(2 * k + 64),
+    if (!lds_chunks_ok(p, k / 32)) return hipErrorInvalidConfiguration;
+    return launch_group(fn, p, g, grid, int4_lds_bytes(p.cw, p.j),
                         static_cast<int>(k / 32), stream);
 }
 
@@ -1545,7 +1584,8 @@ hipError_t launch_q8_group(const Plan& p, const GroupProblem* probs,
     const Q8GroupFn fn = p.block == 512
                              ? instance<Q8LdsGroup<512>>(p.cw, p.j, p.r)
                              : instance<Q8LdsGroup<kBlock>>(p.cw, p.j, p.r);
-    return launch_group(fn, p, g, grid, static_cast<uint32_t>(2 * k + 32),
+    if (!lds_chunks_ok(p, k / 16)) return hipErrorInvalidConfiguration;
+    return launch_group(fn, p, g, grid, q8_lds_bytes(p.cw, p.j),
                         static_cast<int>(k / 16), stream);
 }
 
