@@ -766,10 +766,12 @@ __global__ __launch_bounds__(NT) void qgemv_tiled_kernel(
     const int col = tid & 63;
     const int64_t row0 = (static_cast<int64_t>(xcd_contiguous_block()) * (NT >> 6) + (tid >> 6)) * R;
     const char* wrow[R];
+    float sc[R];   // row scales, loaded first so the final scaling waits on nothing
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint64_t rc = static_cast<uint64_t>(std::min<int64_t>(row0 + r, n - 1));
         wrow[r] = reinterpret_cast<const char*>(w) + rc * (static_cast<uint32_t>(nchunks) * 16u);
+        sc[r] = scale[rc];
     }
     const f16x2 bias = {static_cast<_Float16>(-1152.0f),
                         static_cast<_Float16>(-1152.0f)};
@@ -838,7 +840,7 @@ __global__ __launch_bounds__(NT) void qgemv_tiled_kernel(
     for (int r = 0; r < R; ++r) {
         const float a = segment_sum<64>(acc[r]);
         const int64_t row = row0 + r;
-        if (col == 63 && row < n) y[row] = f2h(scale[row] * a);
+        if (col == 63 && row < n) y[row] = f2h(sc[r] * a);
     }
 }
 
