@@ -164,6 +164,28 @@ def test_tiled_keeps_the_fallbacks():
     assert d["kernel"] == "scalar" and "k above" in d["why"]
 
 
+@pytest.mark.parametrize("op,variants,step", [
+    ("int4gemv", ("int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_lds_r2",
+                  "int4gemv_lds_r4", "int4gemv_wave_r1"), 128),
+    ("qgemv", ("qgemv_cdna4", "qgemv_lds_r1", "qgemv_lds_r2", "qgemv_wave_r1"), 16),
+])
+def test_lds_plans_hold_whole_row_chunks(op, variants, step):
+    """The LDS kernels read a lane's chunks col + cw*j for j < J-1 without a
+    clamp, which stays inside the row only when J = ceil(nchunks / cw); the
+    launch checks it, and every plan must have that form (k up to the
+    untiled limit, both operand widths, several row counts)."""
+    per_chunk = 32 if op == "int4gemv" else 16
+    for variant in variants:
+        for k in range(step, 16384 + 1, step):
+            nchunks = k // per_chunk
+            for n in (1, 4096):
+                d = _capi.describe_launch(op, variant, n, k, 4096, 8192)
+                if d["kernel"] == "scalar":
+                    continue
+                cw, j = int(d["cw"]), int(d["j"])
+                assert j == -(-nchunks // cw), (variant, n, k, d)
+
+
 def test_q8_launch_plans():
     d = _capi.describe_launch("qgemv", "qgemv_cdna4", 4096, 4096, 4096, 8192)
     assert (d["kernel"], d["cw"], d["j"], d["r"]) == ("lds", "64", "4", "1")
