@@ -89,6 +89,25 @@ def test_full_size_bit_exact_properties(ext4, N, K):
         assert torch.equal(yp, y[perm]), v
 
 
+LDS_VARIANTS = ("int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_lds_r2", "int4gemv_lds_r4")
+
+
+@pytest.mark.parametrize("N,K", EDGE + BENCH + EXTRA)
+def test_lds_variants_bit_identical(ext4, N, K):
+    """The LDS kernels sum each row in one lane segment, chunk by chunk in the
+    same order, whatever the rows per lane and workgroup size (and past
+    k = 16384 the K-tiled kernel keeps that order): every LDS variant gives
+    the same bits, including lanes past the row end (clamped last chunk
+    against the zero column of x) and partial last workgroups."""
+    for mode in ("normal", "mixed_sign", "large"):
+        w, s, x = _inputs(N, K, mode, seed=3)
+        ref = ext4.forward("int4gemv_lds_r1", w, s, x)
+        for v in LDS_VARIANTS:
+            announce(f"int4 lds identity {v} N={N} K={K} mode={mode}")
+            y = ext4.forward(v, w, s, x)
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), (v, N, K, mode)
+
+
 @pytest.mark.parametrize("N,K", [(4096, 4096), (11008, 4096), (33, 1024)])
 def test_misaligned_fallback_bit_identical(ext4, N, K):
     """W_packed and x both 2 bytes past a 16-byte boundary (and each alone):

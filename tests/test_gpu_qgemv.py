@@ -70,6 +70,25 @@ def test_full_size_bit_exact_properties(ext8, N, K):
         assert torch.equal(yp, y[perm]), v
 
 
+LDS_VARIANTS = ("qgemv_cdna4", "qgemv_lds_r1", "qgemv_lds_r2", "qgemv_lds_r4")
+
+
+@pytest.mark.parametrize("N,K", EDGE + BENCH + EXTRA)
+def test_lds_variants_bit_identical(ext8, N, K):
+    """The LDS kernels sum each row in one lane segment, chunk by chunk in the
+    same order, whatever the rows per lane and workgroup size (and past
+    k = 16384 the K-tiled kernel keeps that order): every LDS variant gives
+    the same bits, including lanes past the row end (clamped last chunk
+    against the zero column of x) and partial last workgroups."""
+    for mode in ("normal", "mixed_sign", "large"):
+        w, s, x = _inputs(N, K, mode, seed=3)
+        ref = ext8.forward("qgemv_lds_r1", w, s, x)
+        for v in LDS_VARIANTS:
+            announce(f"int8 lds identity {v} N={N} K={K} mode={mode}")
+            y = ext8.forward(v, w, s, x)
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), (v, N, K, mode)
+
+
 @pytest.mark.parametrize("N,K", [(4096, 4096), (64, 13), (11008, 4096)])
 def test_misaligned_fallback_bit_identical(ext8, N, K):
     wq, s, x = _inputs(N, K, "normal", seed=9)
