@@ -689,13 +689,13 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
     const cq::Plan p = make_plan(op, *v, n, k, w, x);
     char line[512];
     std::snprintf(line, sizeof line,
-                  "variant=%s kernel=%s cw=%d j=%d r=%d block=%d grid=%lld fallback=%d why=%s",
+                  "variant=%s kernel=%s cw=%d j=%d r=%d tile=%d block=%d grid=%lld fallback=%d why=%s",
                   v->name,
                   p.kind == cq::kScalar ? "scalar"
                   : p.kind == cq::kLds  ? "lds"
                   : p.kind == cq::kTiled ? "tiled"
                                          : "wave",
-                  p.cw, p.j, p.r,
+                  p.cw, p.j, p.r, p.tile,
                   p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
                   p.why.empty() ? "-" : p.why.c_str());
     return write_out(line, buf, cap);

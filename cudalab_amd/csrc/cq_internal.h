@@ -28,6 +28,7 @@ struct Plan {
     int cw = 0;           // lanes per row segment (16, 32 or 64)
     int j = 0;            // chunks held per lane (x registers)
     int r = 0;            // rows per lane
+    int tile = 0;         // chunks per lane per tile (K-tiled kernels), else 0
     int block = 0;        // threads per workgroup
     int64_t grid = 0;     // workgroups
     bool fallback = false;  // requested a wave variant, got the scalar kernel

@@ -844,16 +844,23 @@ __global__ __launch_bounds__(NT) void qgemv_tiled_kernel(
     }
 }
 
-// Tile size of the K-tiled kernels (chunks per lane per tile), by rows per
-// wave.  Measured on MI355X over HBM-cold pools (k = 28672 .. 65536, n =
-// 1024 .. 16384): two rows per wave do best with 4 chunks per lane per
-// tile (INT4 8192x28672: 24.4 us against 29.3 us with one row and 8), one
-// row per wave with 8; 256-thread workgroups throughout.
-constexpr int tile_j(int r) { return r == 2 ? 4 : 8; }
-// LDS bytes of one tile: `pieces` 16-byte x pieces per chunk (INT4 4, INT8
-// 2), plus the zero column.
-constexpr uint32_t tile_lds(int pieces, int r) {
-    return static_cast<uint32_t>(pieces) * (tile_j(r) * 64 + 1) * 16u;
+// Tile size of the K-tiled kernels (chunks per lane per tile); 256-thread
+// workgroups throughout.  Measured on MI355X over HBM-cold pools, every
+// instance bit-identical:
+// - INT4, one row per wave: 7 chunks per lane per tile.  Against 8 it avoids
+//   a small last tile (k = 28672 splits into two full tiles of 7): 10-13%
+//   faster at 512..3072 x 28672, 1-3% at k = 20480 and 53248, level at 65536.
+// - INT4, two rows per wave: 2 chunks per lane per tile while the row has at
+//   most 16 chunks per lane (k <= 32768, at most 8 tiles): 2-8% faster than 4
+//   at 4096..16384 x 20480..28672; with more tiles the barriers cost more
+//   than the smaller tile saves (4096x65536: 5% slower), so 4 there.
+// - INT8: two rows per wave with 4 chunks per lane per tile, one row with 8.
+constexpr int int4_tile_j(int r, int j) { return r == 1 ? 7 : (j <= 16 ? 2 : 4); }
+constexpr int q8_tile_j(int r) { return r == 2 ? 4 : 8; }
+// LDS bytes of one tile of `tj` chunks per lane: `pieces` 16-byte x pieces
+// per chunk (INT4 4, INT8 2), plus the zero column.
+constexpr uint32_t tile_lds(int pieces, int tj) {
+    return static_cast<uint32_t>(pieces) * (tj * 64 + 1) * 16u;
 }
 
 // Several independent problems of one k per launch (grouped GEMV).  The
@@ -1339,14 +1346,17 @@ Plan scalar_plan(int64_t n, bool fallback, const char* why) {
 }
 
 // The K-tiled kernel: `rows` rows per wave if requested (1 or 2), else two
-// from n = 2048 on (the grid then still has a 256-thread workgroup for
-// every CU) and one below.
-Plan tiled_plan(int rows, int64_t n, int64_t nchunks) {
+// from n = 4096 (INT4) or 2048 (INT8) on and one below.  INT4 at 2048 and
+// 3072 x 28672 with one row and 7-chunk tiles: 10-11% faster than two rows
+// (a grid of one or two workgroups per CU keeps more bytes in flight with
+// the longer tile); from 4096 rows two rows with 2-chunk tiles are faster.
+Plan tiled_plan(int rows, int64_t n, int64_t nchunks, bool int4) {
     Plan p;
     p.kind = kTiled;
     p.cw = 64;
     p.j = static_cast<int>((nchunks + 63) / 64);
-    p.r = rows > 0 ? std::min(rows, 2) : (n >= 2048 ? 2 : 1);
+    p.r = rows > 0 ? std::min(rows, 2) : (n >= (int4 ? 4096 : 2048) ? 2 : 1);
+    p.tile = int4 ? int4_tile_j(p.r, p.j) : q8_tile_j(p.r);
     p.block = kBlock;
     const int64_t waves = (n + p.r - 1) / p.r;
     p.grid = (waves + kBlock / 64 - 1) / (kBlock / 64);
@@ -1378,7 +1388,7 @@ Plan plan_int4(int kind, int rows, int64_t n, int64_t k, const void* w,
     // kernel keeps 64-bit row bases, so it also takes weights of 4 GiB or more
     const bool big = n * (k / 2) >= (int64_t{1} << 32);
     if (kind == kTiled || (kind == kLds && (k > kMaxWaveK || big)))
-        return tiled_plan(rows, n, nchunks);
+        return tiled_plan(rows, n, nchunks, true);
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
@@ -1399,7 +1409,7 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
     const int64_t nchunks = k / 16;
     const bool big = n * k >= (int64_t{1} << 32);    // as in plan_int4
     if (kind == kTiled || (kind == kLds && (k > kMaxWaveK || big)))
-        return tiled_plan(rows, n, nchunks);
+        return tiled_plan(rows, n, nchunks, false);
     if (k > kMaxWaveK) return scalar_plan(n, true, "k above the wave kernels' register-resident x");
     Plan p;
     p.kind = kind;
@@ -1421,14 +1431,19 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
                       static_cast<const uint16_t*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    if (p.kind == kTiled)
-        return launch(p.r == 2 ? int4gemv_tiled_kernel<kBlock, tile_j(2), 2>
-                               : int4gemv_tiled_kernel<kBlock, tile_j(1), 1>,
-                      p.grid, kBlock, tile_lds(4, p.r), stream, ev0, ev1,
+    if (p.kind == kTiled) {
+        const Int4Fn tfn =
+            p.r == 1 && p.tile == 7   ? &int4gemv_tiled_kernel<kBlock, 7, 1>
+            : p.r == 2 && p.tile == 2 ? &int4gemv_tiled_kernel<kBlock, 2, 2>
+            : p.r == 2 && p.tile == 4 ? &int4gemv_tiled_kernel<kBlock, 4, 2>
+                                      : nullptr;
+        if (tfn == nullptr) return hipErrorInvalidConfiguration;
+        return launch(tfn, p.grid, kBlock, tile_lds(4, p.tile), stream, ev0, ev1,
                       static_cast<const uint4*>(w),
                       static_cast<const uint16_t*>(scale),
                       static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
                       static_cast<int>(n), static_cast<int>(k / 32));
+    }
     const Int4Fn fn =
         p.kind == kWave ? instance<Int4Wave>(p.cw, p.j, p.r)
         : p.block == 512 ? instance<Int4Lds<512>>(p.cw, p.j, p.r)
@@ -1452,13 +1467,16 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
                       static_cast<const float*>(scale),
                       static_cast<const uint16_t*>(x),
                       static_cast<uint16_t*>(y), k);
-    if (p.kind == kTiled)
-        return launch(p.r == 2 ? qgemv_tiled_kernel<kBlock, tile_j(2), 2>
-                               : qgemv_tiled_kernel<kBlock, tile_j(1), 1>,
-                      p.grid, kBlock, tile_lds(2, p.r), stream, ev0, ev1,
+    if (p.kind == kTiled) {
+        const Q8Fn tfn = p.r == 2 && p.tile == q8_tile_j(2) ? &qgemv_tiled_kernel<kBlock, q8_tile_j(2), 2>
+                         : p.r == 1 && p.tile == q8_tile_j(1) ? &qgemv_tiled_kernel<kBlock, q8_tile_j(1), 1>
+                                                               : nullptr;
+        if (tfn == nullptr) return hipErrorInvalidConfiguration;
+        return launch(tfn, p.grid, kBlock, tile_lds(2, p.tile), stream, ev0, ev1,
                       static_cast<const uint4*>(w), static_cast<const float*>(scale),
                       static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
                       static_cast<int>(n), static_cast<int>(k / 16));
+    }
     const Q8Fn fn = p.kind == kWave ? instance<Q8Wave>(p.cw, p.j, p.r)
                     : p.block == 512 ? instance<Q8Lds<512>>(p.cw, p.j, p.r)
                                      : instance<Q8Lds<kBlock>>(p.cw, p.j, p.r);
@@ -1621,6 +1639,7 @@ Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
         p.cw = 64;
         p.j = static_cast<int>((nchunks + 63) / 64);
         p.r = 1;
+        p.tile = kGemvTileJ;
         p.block = rounds_ok_512(n) ? 512 : kBlock;
         p.grid = (n + p.block / 64 - 1) / (p.block / 64);
         return p;

@@ -123,27 +123,47 @@ def test_int4_plans_fall_back_to_scalar():
     assert d["kernel"] == "lds"
 
 
-@pytest.mark.parametrize("op,variant,n,k,j,r", [
+@pytest.mark.parametrize("op,variant,n,k,j,r,tile", [
     # k above 16384: the LDS variants run the K-tiled kernel on 256-thread
-    # workgroups, two rows per wave from n = 2048 on, one below
-    ("int4gemv", "int4gemv_cdna4", 8, 16512, 9, 1),
-    ("int4gemv", "int4gemv_cdna4", 8192, 28672, 14, 2),
-    ("int4gemv", "int4gemv_cdna4", 2047, 28672, 14, 1),
-    ("int4gemv", "int4gemv_lds_r2", 100, 20480, 10, 2),     # rows requested
-    ("int4gemv", "int4gemv_lds_r1", 8192, 20480, 10, 1),
-    ("int4gemv", "int4gemv_cdna4", 2048, 65536, 32, 2),
-    ("qgemv", "qgemv_cdna4", 8192, 28672, 28, 2),
-    ("qgemv", "qgemv_cdna4", 3, 16400, 17, 1),
+    # workgroups.  INT4: two rows per wave from n = 4096 on, with 2-chunk
+    # tiles up to 16 chunks per lane and 4-chunk tiles beyond; one row below
+    # 4096 with 7-chunk tiles.  INT8: two rows from n = 2048 on with 4-chunk
+    # tiles, one row below with 8-chunk tiles.
+    ("int4gemv", "int4gemv_cdna4", 8, 16512, 9, 1, 7),
+    ("int4gemv", "int4gemv_cdna4", 8192, 28672, 14, 2, 2),
+    ("int4gemv", "int4gemv_cdna4", 4096, 32768, 16, 2, 2),
+    ("int4gemv", "int4gemv_cdna4", 4096, 32896, 17, 2, 4),
+    ("int4gemv", "int4gemv_cdna4", 4095, 28672, 14, 1, 7),
+    ("int4gemv", "int4gemv_cdna4", 2047, 28672, 14, 1, 7),
+    ("int4gemv", "int4gemv_lds_r2", 100, 20480, 10, 2, 2),     # rows requested
+    ("int4gemv", "int4gemv_lds_r1", 8192, 20480, 10, 1, 7),
+    ("int4gemv", "int4gemv_cdna4", 2048, 65536, 32, 1, 7),
+    ("int4gemv", "int4gemv_cdna4", 16384, 65536, 32, 2, 4),
+    ("qgemv", "qgemv_cdna4", 8192, 28672, 28, 2, 4),
+    ("qgemv", "qgemv_cdna4", 2048, 28672, 28, 2, 4),
+    ("qgemv", "qgemv_cdna4", 3, 16400, 17, 1, 8),
     # the *_lds_tiled variants force it at any k
-    ("int4gemv", "int4gemv_lds_tiled", 4096, 4096, 2, 2),
-    ("int4gemv", "int4gemv_lds_tiled", 1, 128, 1, 1),
-    ("qgemv", "qgemv_lds_tiled", 4097, 11008, 11, 2),
+    ("int4gemv", "int4gemv_lds_tiled", 4096, 4096, 2, 2, 2),
+    ("int4gemv", "int4gemv_lds_tiled", 1, 128, 1, 1, 7),
+    ("qgemv", "qgemv_lds_tiled", 4097, 11008, 11, 2, 4),
 ])
-def test_tiled_plans(op, variant, n, k, j, r):
+def test_tiled_plans(op, variant, n, k, j, r, tile):
     d = _capi.describe_launch(op, variant, n, k, 4096, 8192)
     assert d["kernel"] == "tiled" and d["fallback"] == "0"
     assert (int(d["cw"]), int(d["j"]), int(d["r"]), int(d["block"])) == (64, j, r, 256)
+    assert int(d["tile"]) == tile
     assert int(d["grid"]) == -(-(-(-n // r)) // 4)
+
+
+def test_fp16_tiled_plan_reports_its_tile():
+    d = _capi.describe_launch("gemv_f16", "gemv_lds_tiled", 4096, 4096, 4096, 8192)
+    assert d["kernel"] == "tiled" and d["tile"] == "32"
+
+
+def test_untiled_plans_report_no_tile():
+    for op, variant, k in (("int4gemv", "int4gemv_cdna4", 4096), ("qgemv", "qgemv_cdna4", 4096),
+                           ("int4gemv", "int4gemv_baseline", 4096), ("gemv_f16", "gemv_cdna4", 4096)):
+        assert _capi.describe_launch(op, variant, 4096, k, 4096, 8192)["tile"] == "0", variant
 
 
 def test_tiled_keeps_the_fallbacks():
