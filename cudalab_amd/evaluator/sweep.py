@@ -77,7 +77,7 @@ def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
            "pool_sets": len(sets), "bytes_per_call": nbytes,
            "us_per_call": round(us, 4), "GBps": round(nbytes / us / 1e3, 1),
            "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-           "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r", "block", "grid")}}
+           "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r", "tile", "block", "grid")}}
     if mode == "streaming":
         c = read_ceiling(nbytes, warmup=warmup, n_launches=steps)
         rec["ceiling_us"] = round(c["us_per_call"], 4)
@@ -107,7 +107,9 @@ def table(records: list[dict]) -> str:
              f"{'GB/s':>7} {'%peak':>6} {'ceil_us':>8} {'%ceil':>6}  plan"]
     for r in records:
         p = r["plan"]
-        plan = f"{p['kernel']} cw={p['cw']} j={p['j']} r={p['r']} block={p['block']} grid={p['grid']}"
+        tile = f" tile={p['tile']}" if p.get("tile", "0") != "0" else ""
+        plan = (f"{p['kernel']} cw={p['cw']} j={p['j']} r={p['r']}{tile} "
+                f"block={p['block']} grid={p['grid']}")
         ceil = (f"{r['ceiling_us']:>8.3f} {100 * r['frac_ceiling']:>5.1f}%"
                 if "ceiling_us" in r else f"{'-':>8} {'-':>6}")
         lines.append(f"{r['variant']:<20} {r['N']:>6} {r['K']:>6} {r['mode']:<9} "
