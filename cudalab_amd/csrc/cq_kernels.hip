@@ -848,13 +848,15 @@ __global__ __launch_bounds__(NT) void qgemv_tiled_kernel(
 // workgroups throughout.  Measured on MI355X over HBM-cold pools, every
 // instance bit-identical:
 // - INT4, one row per wave: 7 chunks per lane per tile.  Against 8 it avoids
-//   a small last tile (k = 28672 splits into two full tiles of 7): 10-13%
-//   faster at 512..3072 x 28672, 1-3% at k = 20480 and 53248, level at 65536.
+//   a small last tile (k = 28672 splits into two full tiles of 7): 1-13%
+//   faster at 512..3072 x 20480..53248, level at 65536.
 // - INT4, two rows per wave: 2 chunks per lane per tile while the row has at
 //   most 16 chunks per lane (k <= 32768, at most 8 tiles): 2-8% faster than 4
 //   at 4096..16384 x 20480..28672; with more tiles the barriers cost more
 //   than the smaller tile saves (4096x65536: 5% slower), so 4 there.
-// - INT8: two rows per wave with 4 chunks per lane per tile, one row with 8.
+// - INT8 (tiles of an even number of chunks, so that a tile's x pieces
+//   divide over the workgroup): two rows per wave with 4 chunks per lane
+//   per tile, one row with 8.  2, 6 and 14 were no faster (14 spills).
 constexpr int int4_tile_j(int r, int j) { return r == 1 ? 7 : (j <= 16 ? 2 : 4); }
 constexpr int q8_tile_j(int r) { return r == 2 ? 4 : 8; }
 // LDS bytes of one tile of `tj` chunks per lane: `pieces` 16-byte x pieces
@@ -1345,17 +1347,19 @@ Plan scalar_plan(int64_t n, bool fallback, const char* why) {
     return p;
 }
 
-// The K-tiled kernel: `rows` rows per wave if requested (1 or 2), else two
-// from n = 4096 (INT4) or 2048 (INT8) on and one below.  INT4 at 2048 and
-// 3072 x 28672 with one row and 7-chunk tiles: 10-11% faster than two rows
-// (a grid of one or two workgroups per CU keeps more bytes in flight with
-// the longer tile); from 4096 rows two rows with 2-chunk tiles are faster.
+// The K-tiled kernel: `rows` rows per wave if requested (1 or 2), else one
+// up to n = 3072 and two above.  Up to 3072 rows one row per wave (n / 4
+// workgroups, at most 3 per CU) with the longer tile keeps more bytes in
+// flight: INT4 2048 and 3072 x 28672 10-11% faster than two rows, INT8
+// 2048x28672 15%, 2048x65536 13%, 3072x28672 level.  From 3328 rows two rows
+// per wave are faster for both (INT4 3328x28672 7%, INT8 3328x28672 11%,
+// 3584x65536 6%): one row would leave a fourth, partial workgroup on some CUs.
 Plan tiled_plan(int rows, int64_t n, int64_t nchunks, bool int4) {
     Plan p;
     p.kind = kTiled;
     p.cw = 64;
     p.j = static_cast<int>((nchunks + 63) / 64);
-    p.r = rows > 0 ? std::min(rows, 2) : (n >= (int4 ? 4096 : 2048) ? 2 : 1);
+    p.r = rows > 0 ? std::min(rows, 2) : (n > 3072 ? 2 : 1);
     p.tile = int4 ? int4_tile_j(p.r, p.j) : q8_tile_j(p.r);
     p.block = kBlock;
     const int64_t waves = (n + p.r - 1) / p.r;

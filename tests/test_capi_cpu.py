@@ -125,22 +125,25 @@ def test_int4_plans_fall_back_to_scalar():
 
 @pytest.mark.parametrize("op,variant,n,k,j,r,tile", [
     # k above 16384: the LDS variants run the K-tiled kernel on 256-thread
-    # workgroups.  INT4: two rows per wave from n = 4096 on, with 2-chunk
-    # tiles up to 16 chunks per lane and 4-chunk tiles beyond; one row below
-    # 4096 with 7-chunk tiles.  INT8: two rows from n = 2048 on with 4-chunk
-    # tiles, one row below with 8-chunk tiles.
+    # workgroups.  INT4: two rows per wave above n = 3072, with 2-chunk
+    # tiles up to 16 chunks per lane and 4-chunk tiles beyond; one row up to
+    # 3072 with 7-chunk tiles.  INT8: two rows above 3072 with 4-chunk tiles,
+    # one row up to 3072 with 8-chunk tiles.
     ("int4gemv", "int4gemv_cdna4", 8, 16512, 9, 1, 7),
     ("int4gemv", "int4gemv_cdna4", 8192, 28672, 14, 2, 2),
     ("int4gemv", "int4gemv_cdna4", 4096, 32768, 16, 2, 2),
     ("int4gemv", "int4gemv_cdna4", 4096, 32896, 17, 2, 4),
-    ("int4gemv", "int4gemv_cdna4", 4095, 28672, 14, 1, 7),
+    ("int4gemv", "int4gemv_cdna4", 3073, 28672, 14, 2, 2),
+    ("int4gemv", "int4gemv_cdna4", 3072, 28672, 14, 1, 7),
     ("int4gemv", "int4gemv_cdna4", 2047, 28672, 14, 1, 7),
     ("int4gemv", "int4gemv_lds_r2", 100, 20480, 10, 2, 2),     # rows requested
     ("int4gemv", "int4gemv_lds_r1", 8192, 20480, 10, 1, 7),
     ("int4gemv", "int4gemv_cdna4", 2048, 65536, 32, 1, 7),
     ("int4gemv", "int4gemv_cdna4", 16384, 65536, 32, 2, 4),
     ("qgemv", "qgemv_cdna4", 8192, 28672, 28, 2, 4),
-    ("qgemv", "qgemv_cdna4", 2048, 28672, 28, 2, 4),
+    ("qgemv", "qgemv_cdna4", 4096, 28672, 28, 2, 4),
+    ("qgemv", "qgemv_cdna4", 2048, 28672, 28, 1, 8),
+    ("qgemv", "qgemv_cdna4", 3328, 28672, 28, 2, 4),
     ("qgemv", "qgemv_cdna4", 3, 16400, 17, 1, 8),
     # the *_lds_tiled variants force it at any k
     ("int4gemv", "int4gemv_lds_tiled", 4096, 4096, 2, 2, 2),
