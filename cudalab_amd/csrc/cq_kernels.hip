@@ -633,8 +633,9 @@ __global__ __launch_bounds__(NT) void qgemv_lds_kernel(
 // K-tiled LDS kernels, for rows longer than one batch of chunks held per
 // lane (k > 16384; the *_lds_tiled variants force them at any k).  R rows
 // per wave (CW = 64), both read against one copy of x.  x is staged tile by
-// tile: TJ * 64 chunks of the row per tile (16384 INT4 or 8192 INT8
-// elements), re-paired in LDS, with a barrier before the tile is read and
+// tile: TJ * 64 chunks of the row per tile (TJ = 2..8: TJ * 2048 INT4 or
+// TJ * 1024 INT8 elements), re-paired in LDS, with a barrier before the
+// tile is read and
 // one before the next tile overwrites it.  Every thread of the workgroup
 // runs the same tiles (they depend on nchunks only; rows past n are
 // clamped, never skipped), so every barrier is reached by all.  In the last,
