@@ -635,8 +635,7 @@ __global__ __launch_bounds__(NT) void qgemv_lds_kernel(
 // per wave (CW = 64), both read against one copy of x.  x is staged tile by
 // tile: TJ * 64 chunks of the row per tile (TJ = 2..8: TJ * 2048 INT4 or
 // TJ * 1024 INT8 elements), re-paired in LDS, with a barrier before the
-// tile is read and
-// one before the next tile overwrites it.  Every thread of the workgroup
+// tile is read and one before the next tile overwrites it.  Every thread of the workgroup
 // runs the same tiles (they depend on nchunks only; rows past n are
 // clamped, never skipped), so every barrier is reached by all.  In the last,
 // partial tile only the first ceil(tc / 64) chunks of each lane are loaded
