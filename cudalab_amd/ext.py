@@ -23,6 +23,19 @@ import torch
 
 from . import _capi
 
+
+def _on_device(dev: torch.device, call):
+    """call(stream) with `stream` the raw handle of `dev`'s current HIP
+    stream and `dev` the current device (a launch must be issued with its
+    stream's device current).  The usual case -- `dev` already current --
+    takes the raw handle directly, about 3 us per call cheaper than entering
+    torch.cuda.device and building a Stream object."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if torch.cuda.current_device() == idx:
+        return call(torch._C._cuda_getCurrentRawStream(idx))
+    with torch.cuda.device(idx):
+        return call(torch._C._cuda_getCurrentRawStream(idx))
+
 NATIVE_TIMING_NOTE = (
     "native kernel-loop caliber: back-to-back launches from C++ between two "
     "HIP events on the current stream, window time / launches; no Python "
@@ -129,12 +142,9 @@ class _OpExt:
 
     # ---- launch ----
     def _launch(self, variant: str, W, scale, x, out) -> None:
-        dev = W.device
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = self._fn(variant.encode(), W.data_ptr(), scale.data_ptr(),
-                          x.data_ptr(), out.data_ptr(), W.size(0), self._k(W),
-                          stream)
+        st = _on_device(W.device, lambda stream: self._fn(
+            variant.encode(), W.data_ptr(), scale.data_ptr(), x.data_ptr(),
+            out.data_ptr(), W.size(0), self._k(W), stream))
         if st != _capi.CQ_OK:
             _fail(f"{self.op} launch failed (status {st}): "
                   f"{_capi.last_error()}")
@@ -189,10 +199,8 @@ class _OpExt:
             arr[i].x = x.data_ptr()
             arr[i].y = out.data_ptr()
             arr[i].n = W.size(0)
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = self._grouped_fn(variant.encode(), arr, len(problems), K,
-                                  stream)
+        st = _on_device(dev, lambda stream: self._grouped_fn(
+            variant.encode(), arr, len(problems), K, stream))
         if st != _capi.CQ_OK:
             _fail(f"{self.op} grouped launch failed (status {st}): "
                   f"{_capi.last_error()}")
@@ -214,14 +222,11 @@ class _OpExt:
         self._validate_out(W, out)
         win = (ctypes.c_double * n_windows)()
         res = _capi.CqTiming()
-        dev = W.device
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = self._lib.cq_native_timing(
+        st = _on_device(W.device, lambda stream: self._lib.cq_native_timing(
                 _capi.OPS[self.op], variant.encode(), W.data_ptr(),
                 scale.data_ptr(), x.data_ptr(), out.data_ptr(), W.size(0),
                 self._k(W), stream, warmup, n_windows, launches_per_window,
-                win, ctypes.byref(res))
+                win, ctypes.byref(res)))
         if st != _capi.CQ_OK:
             _fail(f"native_timing failed (status {st}): {_capi.last_error()}")
         return {
@@ -467,10 +472,9 @@ class GemvExt(_OpExt):
         dev = W.device
         dt = (_capi.CQ_DTYPE_F32 if W.dtype == torch.float32
               else _capi.CQ_DTYPE_F16)
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = self._fn(variant.encode(), dt, W.data_ptr(), x.data_ptr(),
-                          out.data_ptr(), W.size(0), W.size(1), stream)
+        st = _on_device(dev, lambda stream: self._fn(
+            variant.encode(), dt, W.data_ptr(), x.data_ptr(), out.data_ptr(),
+            W.size(0), W.size(1), stream))
         if st != _capi.CQ_OK:
             _fail(f"gemv launch failed (status {st}): {_capi.last_error()}")
 
@@ -513,13 +517,10 @@ class GemvExt(_OpExt):
         self._validate_out(W, out)
         win = (ctypes.c_double * n_windows)()
         res = _capi.CqTiming()
-        dev = W.device
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            st = self._lib.cq_native_timing(
+        st = _on_device(W.device, lambda stream: self._lib.cq_native_timing(
                 self._op_id(W), variant.encode(), W.data_ptr(), None,
                 x.data_ptr(), out.data_ptr(), W.size(0), W.size(1), stream,
-                warmup, n_windows, launches_per_window, win, ctypes.byref(res))
+                warmup, n_windows, launches_per_window, win, ctypes.byref(res)))
         if st != _capi.CQ_OK:
             _fail(f"native_timing failed (status {st}): {_capi.last_error()}")
         return {
@@ -648,11 +649,9 @@ def launch_floor(grid: int, block: int, warmup: int = 200,
 def _quant_launch(fn, what: str, W: torch.Tensor, q: torch.Tensor,
                   scale: torch.Tensor, rcp: bool) -> None:
     mode = _capi.CQ_SCALE_RCP if rcp else _capi.CQ_SCALE_DIV
-    dev = W.device
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        st = fn(W.data_ptr(), q.data_ptr(), scale.data_ptr(), W.size(0),
-                W.size(1), mode, stream)
+    st = _on_device(W.device, lambda stream: fn(
+        W.data_ptr(), q.data_ptr(), scale.data_ptr(), W.size(0), W.size(1),
+        mode, stream))
     if st != _capi.CQ_OK:
         _fail(f"{what} failed (status {st}): {_capi.last_error()}")
 
