@@ -1,9 +1,10 @@
 """GPU tests of the grouped GEMV entry points (cq_int4gemv_grouped,
 cq_qgemv_grouped): every output of a grouped call is bit-identical to a
 single forward_into of the same variant on the same problem, for groups
-of one to nine problems (two launches past eight), mixed row counts, and
-batches where one problem misses the vector contract; and within the
-reference's accumulation bound against the oracle."""
+of one to nine problems (two launches past eight), mixed row counts,
+batches where one problem misses the vector contract, and rows longer than
+the untiled kernels take; and within the reference's accumulation bound
+against the oracle."""
 from __future__ import annotations
 
 import numpy as np
@@ -113,6 +114,21 @@ def test_q8_grouped_odd_k_falls_back(ext8):
     outs = _check(ext8, "qgemv_cdna4", probs)
     for (W, s, x), y in zip(probs, outs):
         assert torch.equal(y, ext8.forward("qgemv_baseline", W, s, x))
+
+
+def test_grouped_long_k_runs_problem_by_problem(ext4, ext8):
+    """K above the untiled kernels' limit (16384): a grouped call launches
+    each problem on its own K-tiled kernel, bit-identical to single calls,
+    on both sides of the tiled plans' 3072-row boundary (one row per wave
+    up to 3072 rows, two above) and for a few-row problem."""
+    probs = [_int4_problem(N, 28672, seed=61 + i) for i, N in enumerate((3072, 3073, 5))]
+    for v in ("int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_lds_r2"):
+        announce(f"int4 grouped long-k {v}")
+        _check(ext4, v, probs)
+    probs8 = [_q8_problem(N, 20480, seed=71 + i) for i, N in enumerate((3072, 3073, 7))]
+    for v in ("qgemv_cdna4", "qgemv_lds_r1", "qgemv_lds_r2"):
+        announce(f"q8 grouped long-k {v}")
+        _check(ext8, v, probs8)
 
 
 def test_grouped_rejects_dependent_problems(ext4, ext8):
