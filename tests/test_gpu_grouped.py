@@ -122,13 +122,23 @@ def test_grouped_long_k_runs_problem_by_problem(ext4, ext8):
     on both sides of the tiled plans' 3072-row boundary (one row per wave
     up to 3072 rows, two above) and for a few-row problem."""
     probs = [_int4_problem(N, 28672, seed=61 + i) for i, N in enumerate((3072, 3073, 5))]
+    outs = {}
     for v in ("int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_lds_r2"):
         announce(f"int4 grouped long-k {v}")
-        _check(ext4, v, probs)
+        outs[v] = _check(ext4, v, probs)
+    # one or two rows per wave, 7- or 2-chunk tiles: the same lane order,
+    # so the same bits
+    for v, o in outs.items():
+        for a, b in zip(o, outs["int4gemv_lds_r1"]):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), v
     probs8 = [_q8_problem(N, 20480, seed=71 + i) for i, N in enumerate((3072, 3073, 7))]
+    outs8 = {}
     for v in ("qgemv_cdna4", "qgemv_lds_r1", "qgemv_lds_r2"):
         announce(f"q8 grouped long-k {v}")
-        _check(ext8, v, probs8)
+        outs8[v] = _check(ext8, v, probs8)
+    for v, o in outs8.items():
+        for a, b in zip(o, outs8["qgemv_lds_r1"]):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), v
 
 
 def test_grouped_rejects_dependent_problems(ext4, ext8):
