@@ -5,26 +5,36 @@ one MI355X.  Prints ONE JSON line (the driver's contract).
 A step is one GEMV call on one set of inputs.  Streaming mode rotates
 through a pool of distinct (W_packed, scale, x, y) sets totalling more than
 512 MiB, so W is read from HBM on every call (the 256 MB MALL cannot hold
-the pool).  The timed loop runs in native code (cq_pool_timing): K launches
-back to back on one stream between two HIP events, with a barrier +
-torch.cuda.synchronize() on both sides.
+the pool).  The timed loop runs in native code (cq_pool_timing):
 
-  value         algorithmic bytes x K / event time of the timed window
-                (GB/s, whole-job throughput, inputs resident in HBM)
+  1. untimed launches until both --warmup launches and --burn-ms (300 ms)
+     of wall-clock time have passed (the reference's measure_block burns at
+     least 300 ms, cudalab/evaluator/bench.py:294-300), then a sync;
+  2. a bounded on-device wait (one wave, no memory work) during which the
+     host enqueues the whole window, so the window times the GPU and not
+     the host's submission rate (about 2.5-3.5 us per launch on MI355X,
+     close to the GEMV's own 3.4 us);
+  3. the start event, exactly --steps back-to-back launches on one stream,
+     the stop event; barrier + torch.cuda.synchronize() around it all.
+
+  value         algorithmic bytes x K / event time of the window (GB/s,
+                whole-job throughput, inputs resident in HBM)
   us_per_call   event time of the window / K
-  roofline      the kernel's achieved bandwidth: algorithmic bytes per
-                launch / (window time / K), against 8 TB/s.  Per-launch time
-                over a back-to-back window includes the dispatch gap, so this
-                is a lower bound on the kernel's own bandwidth; rocprofv3's
-                per-dispatch average for the same command is committed under
-                profiles/.  `traffic` is the measured HBM bytes per launch
-                from the committed rocprofv3 counter summary, when present.
-                `measured_ceiling` is a plain read of the same bytes per
-                launch (cq_read_ceiling) over an equally cold pool, timed
-                the same way: what one launch of this size can reach.
-                `launch_floor_us` is an empty kernel of the GEMV's grid and
-                workgroup size (cq_launch_floor), timed the same way: the
-                per-dispatch cost inside every call.
+  rocprof_us_per_dispatch
+                the committed rocprofv3 kernel-trace average of the same
+                kernel instance and shape (profiles/, read at run time), when
+                the profile matches the plan that ran
+  roofline      algorithmic bytes / us_per_call against 8 TB/s.  `traffic`
+                is the measured HBM bytes per launch from the committed
+                rocprofv3 counter summary.  `measured_ceiling` is a plain read
+                of the same bytes per launch (cq_read_ceiling) over an equally
+                cold pool in the same window caliber: what one launch of this
+                size can reach.  `launch_floor_us` is an empty kernel of the
+                GEMV's grid and workgroup size, same caliber.
+  detail        the same window (K launches, pre-filled) repeated: INT4
+                streaming, INT4 hot (one resident set), INT8 streaming on the
+                same shape, each the median of 5 windows, and their ratios;
+                plus the hipGraph and grouped (8 GEMVs per launch) calibers
   cpu_baseline  the oracle's fused OpenMP CPU GEMV (oracle/qgemv_oracle.c)
                 on the same shape, timed on this host over a bounded sample:
                 about --cpu-seconds (6 s) of calls cycling over 16 distinct
@@ -32,6 +42,10 @@ torch.cuda.synchronize() on both sides.
                 the same C port on one thread, the reference's torch CPU
                 formulation (dequantize, FP32 torch.mv) on all threads and
                 on one, and the host CPU model (about 13 s of CPU in all)
+
+`--cpu-sweep` instead times the CPU paths alone at the five bench shapes
+(INT4 and INT8; C port and torch formulation; all threads and one) and
+prints one JSON line per shape (no GPU needed).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -55,8 +69,11 @@ TRAFFIC_FILE = ROOT / "profiles" / "int4gemv_4096x4096_streaming_traffic.json"
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--burn-ms", type=float, default=300.0,
+                    help="untimed launches run for at least this long before "
+                         "the window (as well as --warmup launches)")
     ap.add_argument("--variant", default="int4gemv_cdna4")
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--k", type=int, default=4096)
@@ -68,26 +85,84 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-detail", action="store_true",
-                    help="skip the INT8 / hot-mode detail measurements")
+                    help="skip the INT8 / hot-mode / ceiling detail measurements")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB "
                          "(counter calibration runs)")
+    ap.add_argument("--cpu-sweep", action="store_true",
+                    help="time only the CPU paths at the five bench shapes")
     return ap.parse_args(argv)
 
 
-def gpu_loop(op: str, variant: str, sets, steps: int, warmup: int) -> dict:
-    """K back-to-back launches rotating through `sets`, timed by two HIP
-    events around the window (native loop, no per-launch events)."""
+def gpu_loop(op: str, variant: str, sets, steps: int, warmup: int,
+             burn_ms: float) -> dict:
+    """One window of `steps` back-to-back launches rotating through `sets`,
+    pre-filled behind an on-device wait, timed by two HIP events around the
+    window (native loop, no per-launch events)."""
     import torch
-    from cudalab_amd.ext import pool_timing
+    from cudalab_amd.ext import pool_timing, prefill_delay_us
     torch.cuda.synchronize()           # barrier (single rank) + sync
     t0 = time.perf_counter()
     r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
-                    per_kernel=False)
+                    per_kernel=False, burn_ms=burn_ms,
+                    delay_us=prefill_delay_us(steps))
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     return {"total_us": r["total_us"], "us_per_call": r["total_us"] / steps,
-            "wall_s": wall_s}
+            "host_us_per_call": r["host_us"] / steps, "wall_s": wall_s}
+
+
+def windows(op: str, variant: str, sets, steps: int, count: int = 5) -> dict:
+    """`count` more pre-filled windows of `steps` launches (no burn: the
+    caller has just run one); median and spread of µs per call.  The pool
+    rotation continues from window to window (each call of the native loop
+    starts at its list's first set), so a short window never meets sets
+    that the previous one left in the MALL."""
+    from cudalab_amd.ext import pool_timing, prefill_delay_us
+    us = []
+    off = 0
+    for _ in range(count):
+        rot = sets[off:] + sets[:off]
+        r = pool_timing(op, variant, rot, warmup=0, n_launches=steps,
+                        per_kernel=False, delay_us=prefill_delay_us(steps))
+        off = (off + steps) % len(sets)
+        us.append(r["total_us"] / steps)
+    us.sort()
+    return {"median": us[len(us) // 2], "min": us[0], "max": us[-1], "n": count}
+
+
+def kernel_instance(plan: dict) -> str:
+    """Name fragment of the kernel instance a plan launches (as rocprofv3
+    prints it), e.g. 'int4gemv_lds_kernel<64, 2, 1, 512>'."""
+    if plan["kernel"] == "lds":
+        return (f"int4gemv_lds_kernel<{plan['cw']}, {plan['j']}, {plan['r']}, "
+                f"{plan['block']}>")
+    if plan["kernel"] == "tiled":
+        return f"int4gemv_tiled_kernel<256, {plan['tile']}, {plan['r']}>"
+    return f"int4gemv_{plan['kernel']}"
+
+
+def load_rocprof(N: int, K: int, mode: str, plan: dict):
+    """The committed kernel-trace record for this shape, if it is of the
+    kernel instance that ran: (mean µs per dispatch, file name) or
+    (None, reason)."""
+    f = ROOT / "profiles" / f"int4gemv_{N}x{K}_{mode}_kernel_trace.json"
+    if not f.exists():
+        return None, f"no {f.name}"
+    try:
+        d = json.loads(f.read_text())
+    except Exception as e:  # noqa: BLE001
+        return None, f"{f.name}: {e}"
+    want = kernel_instance(plan)
+    if want not in d.get("kernel", "") or d.get("shape") != [N, K]:
+        return None, (f"{f.name} is of {d.get('kernel', '?')[:60]} "
+                      f"{d.get('shape')}, not {want} [{N}, {K}]")
+    return round(float(d["mean_us"]), 4), f"profiles/{f.name}"
+
+
+def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
+    from cudalab_amd.evaluator.sweep import make_sets as _make_sets
+    return _make_sets(op, N, K, mode, seed)
 
 
 def graph_loop(ext, variant: str, sets, per_graph: int = 256,
@@ -143,11 +218,6 @@ def grouped_graph_loop(ext, variant: str, sets, group: int = 8,
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (per_graph * replays * group)
-
-
-def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
-    from cudalab_amd.evaluator.sweep import make_sets as _make_sets
-    return _make_sets(op, N, K, mode, seed)
 
 
 def _timed_calls(fn, min_s: float, min_n: int, max_n: int) -> list[float]:
@@ -261,6 +331,74 @@ def load_traffic(N: int, K: int):
     return None
 
 
+CPU_SWEEP_SHAPES = ((1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096),
+                    (4096, 11008))
+
+
+def cpu_sweep(seconds: float = 1.0) -> int:
+    """The CPU paths at the five bench shapes, INT4 and INT8: the oracle's
+    fused C + OpenMP port on all threads and on one, and the reference's
+    torch CPU formulation (INT4: dequantize_w then an FP32 torch.mv,
+    cudalab/int4gemv_correctness.py:220-221; INT8: W_q.float() * scale then
+    torch.mv, cudalab/qgemv_correctness.py:189) on all threads and on one.
+    Each figure is the median per call of about `seconds` of calls (at least
+    3) on one input set drawn with the bench recipe (W ~ N(0, 0.02)
+    quantized, x ~ N(0, 1)); each result is checked against the oracle's
+    bound first.  One JSON line per (op, shape)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as orc
+    from cudalab_amd.int4gemv_quantize import dequantize_w
+    from cudalab_amd.operators import int4gemv as op4
+    from cudalab_amd.operators import qgemv as op8
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or min(16, os.cpu_count() or 1)
+    host = _host_cpu()
+
+    def med_us(fn, n_min=3):
+        fn()
+        return statistics.median(_timed_calls(lambda i: fn(), seconds, n_min, 100000)) * 1e6
+
+    prev = torch.get_num_threads()
+    try:
+        for op in ("int4gemv", "qgemv"):
+            for (N, K) in CPU_SWEEP_SHAPES:
+                if op == "int4gemv":
+                    wp, sc, x, _ = op4.device_random_set(N, K, 1234 + 100000, device="cpu")
+                    a = (wp.numpy(), sc.numpy(), x.numpy())
+                    y = orc.gemv_w4_cpu(*a, threads)
+                    assert orc.check_w4(y, *a) <= 1.0
+                    c_fn = orc.gemv_w4_cpu
+                    nbytes = op4.int4_bytes(N, K)
+
+                    def t_fn(wp=wp, sc=sc, x=x):
+                        torch.mv(dequantize_w(wp, sc), x.float()).half()
+                else:
+                    wq, sc, x, _ = op8.device_random_set(N, K, 1234 + 100000, device="cpu")
+                    a = (wq.numpy(), sc.numpy(), x.numpy())
+                    y = orc.gemv_w8_cpu(*a, threads)
+                    assert orc.check_w8(y, *a) <= 1.0
+                    c_fn = orc.gemv_w8_cpu
+                    nbytes = op8.q8_bytes(N, K)
+
+                    def t_fn(wq=wq, sc=sc, x=x):
+                        torch.mv(wq.float() * sc[:, None], x.float()).half()
+                rec = {"op": op, "N": N, "K": K, "algorithmic_bytes": nbytes,
+                       "threads": threads}
+                rec["c_port_us"] = round(med_us(lambda: c_fn(*a, threads)), 2)
+                rec["c_port_1_thread_us"] = round(med_us(lambda: c_fn(*a, 1)), 2)
+                torch.set_num_threads(threads)
+                rec["torch_us"] = round(med_us(t_fn), 1)
+                torch.set_num_threads(1)
+                rec["torch_1_thread_us"] = round(med_us(t_fn), 1)
+                torch.set_num_threads(prev)
+                rec["c_port_GBps"] = round(nbytes / rec["c_port_us"] / 1e3, 2)
+                rec["host"] = host
+                print(json.dumps(rec), flush=True)
+    finally:
+        torch.set_num_threads(prev)
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
@@ -269,6 +407,8 @@ def main(argv=None) -> int:
               "row shard of W; only the one-GPU figure is measured)",
               file=sys.stderr)
         return 2
+    if args.cpu_sweep:
+        return cpu_sweep()
     import torch
     from cudalab_amd.build import build
     if not torch.cuda.is_available():
@@ -289,22 +429,36 @@ def main(argv=None) -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
 
-    r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup)
-
-    from cudalab_amd.ext import launch_floor, read_ceiling
-    ceil = read_ceiling(nbytes)
-    floor_us = launch_floor(int(plan["grid"]), int(plan["block"]))
+    r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup,
+                 args.burn_ms)
 
     total_s = r["total_us"] * 1e-6
     value = nbytes * args.steps / total_s / 1e9
     achieved = nbytes / (r["us_per_call"] * 1e-6) / 1e9
     traffic = load_traffic(N, K)
+    rp_us, rp_src = load_rocprof(N, K, args.mode, plan)
 
-    detail = {"plan": plan, "pool_sets": len(sets),
-              "pool_bytes": len(sets) * nbytes,
+    detail = {"plan": plan, "kernel_instance": kernel_instance(plan),
+              "pool_sets": len(sets), "pool_bytes": len(sets) * nbytes,
               "algorithmic_bytes_per_call": nbytes,
-              "wall_s_timed": round(r["wall_s"], 4)}
+              "window": {"launches": args.steps, "warmup_launches_min": args.warmup,
+                         "burn_ms_min": args.burn_ms,
+                         "prefill": "on-device wait queued before the start "
+                                    "event; the host enqueues the window behind it",
+                         "host_enqueue_us_per_call": round(r["host_us_per_call"], 4)},
+              "wall_s_timed": round(r["wall_s"], 4),
+              "rocprof_source": rp_src}
+    ceil = floor_us = None
     if not args.no_detail:
+        from cudalab_amd.ext import launch_floor, prefill_delay_us, read_ceiling
+        nl = max(args.steps, 200)
+        ceil = read_ceiling(nbytes, warmup=args.warmup, n_launches=nl,
+                            burn_ms=100.0, delay_us=prefill_delay_us(nl))
+        floor_us = launch_floor(int(plan["grid"]), int(plan["block"]),
+                                warmup=args.warmup, n_launches=nl, burn_ms=100.0,
+                                delay_us=prefill_delay_us(nl))
+        w4 = windows("int4gemv", args.variant, sets, args.steps)
+        detail["int4_5_windows_us"] = {k: round(v, 4) for k, v in w4.items()}
         detail["graph_us_per_call"] = round(graph_loop(ext4, args.variant, sets), 4)
         if args.mode == "streaming" and len(sets) >= 16:
             gp = grouped_graph_loop(ext4, args.variant, sets)
@@ -312,23 +466,45 @@ def main(argv=None) -> int:
             detail["grouped8_graph_GBps"] = round(nbytes / gp / 1e3, 1)
             detail["grouped8_note"] = ("8 independent GEMVs of this shape per launch "
                                        "(cq_int4gemv_grouped) over distinct HBM-cold "
-                                       "sets, from a HIP graph: the per-launch floor "
+                                       "sets, from a HIP graph: the per-launch cost "
                                        "shared by 8 GEMVs; not the headline caliber")
-        h = gpu_loop("int4gemv", args.variant, sets[:1], 2000, 200)
-        detail["hot_us_per_call"] = round(h["us_per_call"], 4)
-        detail["hot_GBps"] = round(nbytes / h["us_per_call"] / 1e3, 1)
+        gpu_loop("int4gemv", args.variant, sets[:1], args.steps, args.warmup, 100.0)
+        h = windows("int4gemv", args.variant, sets[:1], args.steps)
+        detail["hot_us_per_call"] = round(h["median"], 4)
+        detail["hot_GBps"] = round(nbytes / h["median"] / 1e3, 1)
         build("qgemv")
         q_sets, q_bytes = make_sets("qgemv", N, K, args.mode)
-        q = gpu_loop("qgemv", "qgemv_cdna4", q_sets, 2000, 200)
-        detail["int8_us_per_call"] = round(q["us_per_call"], 4)
-        detail["int8_GBps"] = round(q_bytes / q["us_per_call"] / 1e3, 1)
-        detail["speedup_int4_vs_int8"] = round(q["us_per_call"] / r["us_per_call"], 3)
+        gpu_loop("qgemv", "qgemv_cdna4", q_sets, args.steps, args.warmup, 100.0)
+        q = windows("qgemv", "qgemv_cdna4", q_sets, args.steps)
+        detail["int8_us_per_call"] = round(q["median"], 4)
+        detail["int8_GBps"] = round(q_bytes / q["median"] / 1e3, 1)
+        detail["speedup_int4_vs_int8"] = round(q["median"] / w4["median"], 3)
+        detail["speedup_note"] = ("INT8 and INT4 medians of 5 pre-filled windows of "
+                                  f"{args.steps} launches each, streaming, same shape")
         del q_sets
         torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(N, K, sets, seconds=args.cpu_seconds)
 
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic}
+    if rp_us is not None:
+        roofline["achieved_rocprof"] = round(nbytes / rp_us / 1e3, 1)
+        roofline["frac_rocprof"] = round(nbytes / rp_us / 1e3 / HBM_PEAK_GBS, 4)
+    if ceil is not None:
+        roofline.update({
+            "measured_ceiling": round(ceil["GBps"], 1),
+            "frac_of_measured_ceiling": round(achieved / ceil["GBps"], 4),
+            "ceiling_note": "plain streaming read of the same bytes per launch "
+                            "over an HBM-cold pool (cq_read_ceiling), same "
+                            "pre-filled window caliber",
+            "launch_floor_us": round(floor_us, 4),
+            "floor_note": "back-to-back launches of a kernel with no memory work "
+                          "in the GEMV's launch shape (cq_launch_floor, grid %s x "
+                          "%s threads), same caliber" % (plan["grid"], plan["block"])})
     line = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -338,6 +514,7 @@ def main(argv=None) -> int:
         "warmup": args.warmup,
         "ms_per_step": round(total_s * 1e3 / args.steps, 6),
         "us_per_call": round(r["us_per_call"], 4),
+        "rocprof_us_per_dispatch": rp_us,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -349,23 +526,7 @@ def main(argv=None) -> int:
                    "N": N, "K": K, "group_size": 128,
                    "variant": args.variant, "mode": args.mode,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "measured_ceiling": round(ceil["GBps"], 1),
-                     "frac_of_measured_ceiling": round(achieved / ceil["GBps"], 4),
-                     "ceiling_note": "plain streaming read of the same bytes "
-                                     "per launch over an HBM-cold pool "
-                                     "(cq_read_ceiling), same timed-window "
-                                     "caliber",
-                     "launch_floor_us": round(floor_us, 4),
-                     "floor_note": "back-to-back launches of a kernel with no "
-                                   "memory work in the GEMV's launch shape "
-                                   "(cq_launch_floor, grid %s x %s threads), "
-                                   "same caliber: the per-dispatch cost "
-                                   "included in us_per_call" % (plan["grid"],
-                                                                plan["block"])},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "detail": detail,
     }

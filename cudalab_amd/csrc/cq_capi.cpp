@@ -17,7 +17,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <climits>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <numeric>
@@ -398,6 +400,79 @@ struct Events {
     }
 };
 
+// Options of the timing loops' window (see cq_pool_timing).
+struct Window {
+    int64_t warmup;     // untimed launches, at least
+    double burn_ms;     // and at least this much wall-clock time of them
+    double delay_us;    // > 0: on-device wait queued ahead of the window
+    int64_t n_launches;
+};
+
+int check_window(const Window& w) {
+    if (w.warmup < 0) return fail(CQ_ERR_INVALID_ARG, "warmup must be >= 0");
+    if (w.n_launches < 1) return fail(CQ_ERR_INVALID_ARG, "n_launches must be >= 1");
+    if (!std::isfinite(w.burn_ms) || w.burn_ms < 0 || w.burn_ms > 600000)
+        return fail(CQ_ERR_INVALID_ARG, "burn_ms must be in [0, 600000]");
+    if (!std::isfinite(w.delay_us) || w.delay_us < 0 || w.delay_us > 1e6)
+        return fail(CQ_ERR_INVALID_ARG, "delay_us must be in [0, 1e6]");
+    return CQ_OK;
+}
+
+// The shared timing loop.  `go(i, ev0, ev1)` enqueues launch i (ev0/ev1
+// non-null: events on the dispatch itself).  Untimed launches run until
+// both `warmup` launches and `burn_ms` of wall-clock time have passed
+// (clocks and power settle); the stream is synchronized; a delay of
+// `delay_us` is queued; then the start event, the n_launches timed
+// launches and the stop event.  *total_us is the event time of the window,
+// *host_us (if non-null) the host time spent enqueuing it: a window whose
+// host time reaches its event time was bound by submission, not the GPU.
+template <typename Go>
+int timed_window(Go go, hipStream_t s, const Window& w, float* kernel_us,
+                 double* total_us, double* host_us) {
+    using clock = std::chrono::steady_clock;
+    hipError_t e;
+    const auto t_burn = clock::now();
+    int64_t i = 0;
+    while (i < w.warmup ||
+           std::chrono::duration<double, std::milli>(clock::now() - t_burn).count() < w.burn_ms) {
+        if ((e = go(i, nullptr, nullptr)) != hipSuccess) return hip_fail(e, "warmup launch");
+        ++i;
+    }
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    Events win;
+    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
+    Events per;
+    if (kernel_us != nullptr &&
+        (e = per.make(2 * static_cast<size_t>(w.n_launches))) != hipSuccess)
+        return hip_fail(e, "hipEventCreate");
+    if ((e = cq::launch_delay(w.delay_us, s)) != hipSuccess) return hip_fail(e, "delay launch");
+    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    const auto t_enq = clock::now();
+    for (int64_t j = 0; j < w.n_launches; ++j) {
+        hipEvent_t e0 = kernel_us ? per.ev[2 * static_cast<size_t>(j)] : nullptr;
+        hipEvent_t e1 = kernel_us ? per.ev[2 * static_cast<size_t>(j) + 1] : nullptr;
+        if ((e = go(i + j, e0, e1)) != hipSuccess) return hip_fail(e, "timed launch");
+    }
+    const double enq_us = std::chrono::duration<double, std::micro>(clock::now() - t_enq).count();
+    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
+        return hip_fail(e, "hipEventElapsedTime");
+    if (total_us != nullptr) *total_us = static_cast<double>(ms) * 1e3;
+    if (host_us != nullptr) *host_us = enq_us;
+    if (kernel_us != nullptr) {
+        for (int64_t j = 0; j < w.n_launches; ++j) {
+            float kms = 0.f;
+            e = hipEventElapsedTime(&kms, per.ev[2 * static_cast<size_t>(j)],
+                                    per.ev[2 * static_cast<size_t>(j) + 1]);
+            if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime (kernel)");
+            kernel_us[j] = kms * 1e3f;
+        }
+    }
+    return CQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -526,20 +601,22 @@ int cq_native_timing(int op, const char* variant, const void* w,
 int cq_pool_timing(int op, const char* variant, const void* const* w,
                    const void* const* scale, const void* const* x,
                    void* const* y, int64_t n_sets, int64_t n, int64_t k,
-                   void* stream, int64_t warmup, int64_t n_launches,
-                   float* kernel_us, double* total_us) {
+                   void* stream, int64_t warmup, double burn_ms,
+                   double delay_us, int64_t n_launches, float* kernel_us,
+                   double* total_us, double* host_us) {
     g_last_error.clear();
     if (w == nullptr || (scale == nullptr && !is_gemv(op)) || x == nullptr ||
         y == nullptr)
         return fail(CQ_ERR_INVALID_ARG, "null set array");
     if (n_sets < 1) return fail(CQ_ERR_INVALID_ARG, "n_sets must be >= 1");
-    if (warmup < 0) return fail(CQ_ERR_INVALID_ARG, "warmup must be >= 0");
-    if (n_launches < 1) return fail(CQ_ERR_INVALID_ARG, "n_launches must be >= 1");
+    const Window win{warmup, burn_ms, delay_us, n_launches};
+    int st = check_window(win);
+    if (st != CQ_OK) return st;
     std::vector<cq::Plan> plans(static_cast<size_t>(n_sets));
     const Variant* v = nullptr;
     for (int64_t i = 0; i < n_sets; ++i) {
         const void* sc = scale != nullptr ? scale[i] : nullptr;
-        const int st = check_launch(op, variant, &v, w[i], sc, x[i], y[i], n, k);
+        st = check_launch(op, variant, &v, w[i], sc, x[i], y[i], n, k);
         if (st != CQ_OK) return st;
         plans[static_cast<size_t>(i)] = make_plan(op, *v, n, k, w[i], x[i]);
     }
@@ -549,104 +626,48 @@ int cq_pool_timing(int op, const char* variant, const void* const* w,
         return launch_plan(op, plans[si], w[si], scale != nullptr ? scale[si] : nullptr,
                            x[si], y[si], n, k, s, e0, e1);
     };
-    hipError_t e;
-    for (int64_t i = 0; i < warmup; ++i)
-        if ((e = go(i, nullptr, nullptr)) != hipSuccess) return hip_fail(e, "warmup launch");
-    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-
-    Events win;
-    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
-    Events per;
-    if (kernel_us != nullptr &&
-        (e = per.make(2 * static_cast<size_t>(n_launches))) != hipSuccess)
-        return hip_fail(e, "hipEventCreate");
-    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    for (int64_t i = 0; i < n_launches; ++i) {
-        hipEvent_t e0 = kernel_us ? per.ev[2 * static_cast<size_t>(i)] : nullptr;
-        hipEvent_t e1 = kernel_us ? per.ev[2 * static_cast<size_t>(i) + 1] : nullptr;
-        if ((e = go(warmup + i, e0, e1)) != hipSuccess) return hip_fail(e, "timed launch");
-    }
-    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
-    float ms = 0.f;
-    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
-        return hip_fail(e, "hipEventElapsedTime");
-    if (total_us != nullptr) *total_us = static_cast<double>(ms) * 1e3;
-    if (kernel_us != nullptr) {
-        for (int64_t i = 0; i < n_launches; ++i) {
-            float kms = 0.f;
-            e = hipEventElapsedTime(&kms, per.ev[2 * static_cast<size_t>(i)],
-                                    per.ev[2 * static_cast<size_t>(i) + 1]);
-            if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime (kernel)");
-            kernel_us[i] = kms * 1e3f;
-        }
-    }
-    return CQ_OK;
+    return timed_window(go, s, win, kernel_us, total_us, host_us);
 }
 
 int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
-                    void* sink, void* stream, int64_t warmup,
-                    int64_t n_launches, double* total_us) {
+                    void* sink, void* stream, int64_t warmup, double burn_ms,
+                    double delay_us, int64_t n_launches, double* total_us) {
     g_last_error.clear();
     if (bufs == nullptr || sink == nullptr || total_us == nullptr)
         return fail(CQ_ERR_INVALID_ARG, "null argument");
-    if (n_bufs < 1 || warmup < 0 || n_launches < 1)
-        return fail(CQ_ERR_INVALID_ARG, "n_bufs, n_launches must be >= 1, warmup >= 0");
+    if (n_bufs < 1) return fail(CQ_ERR_INVALID_ARG, "n_bufs must be >= 1");
+    const Window win{warmup, burn_ms, delay_us, n_launches};
+    const int st = check_window(win);
+    if (st != CQ_OK) return st;
     if (bytes < 16 || bytes % 16 != 0)
         return fail(CQ_ERR_INVALID_ARG, "bytes must be a positive multiple of 16");
     for (int64_t i = 0; i < n_bufs; ++i)
         if (bufs[i] == nullptr || (reinterpret_cast<uintptr_t>(bufs[i]) & 15u) != 0)
             return fail(CQ_ERR_INVALID_ARG, "buffers must be non-null and 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    for (int64_t i = 0; i < warmup; ++i)
-        if ((e = cq::launch_stream_read(bufs[i % n_bufs], bytes, sink, s)) != hipSuccess)
-            return hip_fail(e, "warmup launch");
-    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    Events win;
-    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
-    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    for (int64_t i = 0; i < n_launches; ++i)
-        if ((e = cq::launch_stream_read(bufs[(warmup + i) % n_bufs], bytes, sink, s)) != hipSuccess)
-            return hip_fail(e, "timed launch");
-    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
-    float ms = 0.f;
-    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
-        return hip_fail(e, "hipEventElapsedTime");
-    *total_us = static_cast<double>(ms) * 1e3;
-    return CQ_OK;
+    auto go = [&](int64_t i, hipEvent_t, hipEvent_t) {
+        return cq::launch_stream_read(bufs[i % n_bufs], bytes, sink, s);
+    };
+    return timed_window(go, s, win, nullptr, total_us, nullptr);
 }
 
 int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
-                    int64_t warmup, int64_t n_launches, double* total_us) {
+                    int64_t warmup, double burn_ms, double delay_us,
+                    int64_t n_launches, double* total_us) {
     g_last_error.clear();
     if (sink == nullptr || total_us == nullptr)
         return fail(CQ_ERR_INVALID_ARG, "null argument");
-    if (warmup < 0 || n_launches < 1)
-        return fail(CQ_ERR_INVALID_ARG, "n_launches must be >= 1, warmup >= 0");
+    const Window win{warmup, burn_ms, delay_us, n_launches};
+    const int st = check_window(win);
+    if (st != CQ_OK) return st;
     if (grid < 1 || grid > INT_MAX || block < 1 || block > 1024)
         return fail(CQ_ERR_INVALID_ARG,
                     "grid must be in [1, INT_MAX] and block in [1, 1024]");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e;
-    for (int64_t i = 0; i < warmup; ++i)
-        if ((e = cq::launch_empty(grid, block, sink, s)) != hipSuccess)
-            return hip_fail(e, "warmup launch");
-    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    Events win;
-    if ((e = win.make(2)) != hipSuccess) return hip_fail(e, "hipEventCreate");
-    if ((e = hipEventRecord(win.ev[0], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    for (int64_t i = 0; i < n_launches; ++i)
-        if ((e = cq::launch_empty(grid, block, sink, s)) != hipSuccess)
-            return hip_fail(e, "timed launch");
-    if ((e = hipEventRecord(win.ev[1], s)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-    if ((e = hipEventSynchronize(win.ev[1])) != hipSuccess) return hip_fail(e, "hipEventSynchronize");
-    float ms = 0.f;
-    if ((e = hipEventElapsedTime(&ms, win.ev[0], win.ev[1])) != hipSuccess)
-        return hip_fail(e, "hipEventElapsedTime");
-    *total_us = static_cast<double>(ms) * 1e3;
-    return CQ_OK;
+    auto go = [&](int64_t, hipEvent_t, hipEvent_t) {
+        return cq::launch_empty(grid, block, sink, s);
+    };
+    return timed_window(go, s, win, nullptr, total_us, nullptr);
 }
 
 int cq_variants(int op, int which, char* buf, size_t cap) {

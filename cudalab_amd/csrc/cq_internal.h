@@ -112,6 +112,12 @@ hipError_t launch_q8_quantize(const QuantPlan& p, const void* w, void* wq,
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
                               hipStream_t stream);
 
+// A bounded on-device wait of about `us` microseconds (one wave, no
+// memory work), queued ahead of a timed window so that the host can
+// enqueue the window's launches before the GPU reaches them.  No launch
+// when us <= 0.
+hipError_t launch_delay(double us, hipStream_t stream);
+
 // One launch of a kernel with no memory work, `grid` workgroups of `block`
 // threads (1..1024): the per-dispatch cost of that launch shape.
 hipError_t launch_empty(int64_t grid, int block, void* sink,

@@ -1162,6 +1162,22 @@ __global__ __launch_bounds__(1024) void empty_launch_kernel(
     if (threadIdx.x == key) sink[0] = blockIdx.x;
 }
 
+// A bounded on-device wait for the timing loops: one wave sleeps until the
+// constant-rate wall clock has advanced `ticks`, or until it has gone round
+// its loop `max_iters` times, whichever comes first (so it ends even if the
+// clock were not running).  Queued ahead of a timed window it keeps the GPU
+// busy while the host enqueues the window's launches, so the window times
+// the GPU and not the host's submission rate (about 2.5-3.5 us per launch
+// on MI355X, close to a short GEMV's own time).  It touches no memory.
+__global__ __launch_bounds__(64) void delay_kernel(uint64_t ticks,
+                                                   uint64_t max_iters) {
+    const uint64_t t0 = wall_clock64();
+    for (uint64_t i = 0; i < max_iters; ++i) {
+        if (wall_clock64() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(8);
+    }
+}
+
 // --------------------------------------------------------- instance tables
 
 using Int4Fn = void (*)(const uint4*, const uint16_t*, const uint4*,
@@ -1280,32 +1296,34 @@ int pow2_at_least(int64_t v, int lo) {
     return p;
 }
 
-// Default rows per lane (measured on MI355X, streaming, decided with the
-// paired A/B engine): INT4 takes two rows per lane only when each lane
-// holds at most 2 chunks of a row, that leaves at least 2048 waves, and
-// the 512-thread workgroups of that plan fill the CUs in whole rounds
-// (their count a multiple of kCus); otherwise one row on 256-thread
-// workgroups.  4096^2 (256 workgroups): two rows are faster (A/B CI95 of
-// one/two [0.917, 0.991]); 6144x4096 (384): one row is a KEEP at 1.10x;
-// 11008x4096 and 14336x4096: one row level or 0.5-1% faster; with 4
-// chunks per lane (k = 8192) one row is 11-15% faster.  INT8 does best
-// with one row per lane at every bench shape.
+// Default rows per lane (measured on MI355X with kernel arguments
+// preloaded, HBM-cold pools, back-to-back launches on a pre-filled queue;
+// every candidate bit-identical).  INT4 with at most 3 chunks per lane:
+// - rows of at most 32 chunks (64 // CW >= 2 row slots per wave): two rows
+//   (4096x1024: 2.39 us against 2.55);
+// - otherwise one row while one row per wave keeps the whole grid resident
+//   (at most 32 waves per CU on kCus CUs), two above, where one row per wave
+//   would run a second round of waves: 4096^2 one row 3.38 us against two
+//   3.56-3.63; 6144x4096 4.18 against 4.34; 11008x4096 two rows 6.05 against
+//   6.36; 14336x4096 7.41 against 7.65; 13824x5120 9.32 against 10.14.
+// With 4 or more chunks per lane one row throughout (8192^2 8.19 us against
+// 9.01, 28672x8192 24.3 against 25.0).  INT8 does best with one row per lane
+// at every shape measured.
 constexpr int64_t kCus = 256;
+constexpr int64_t kResidentWaves = 32 * kCus;
 int default_rows_int4(int64_t n, int slots, int j, int rmax) {
-    constexpr int64_t min_waves = 2048;
-    if (j > 2 || rmax < 2) return 1;
-    const int64_t waves = (n + slots * 2 - 1) / (slots * 2);
-    const int64_t grid = (waves + 7) / 8;          // 512-thread workgroups
-    return (waves >= min_waves && grid % kCus == 0) ? 2 : 1;
+    if (j > 3 || rmax < 2) return 1;
+    if (slots >= 2) return 2;
+    return n > kResidentWaves ? 2 : 1;
 }
 
 // Workgroup size of the LDS kernels.  512 threads halve the number of
 // workgroups that stage x.  Measured on MI355X (same launch path, HBM-cold
 // pools) this pays when x is large next to each workgroup's weights (INT4
-// with two rows per lane or 3+ chunks per lane, INT8 with 8+ chunks per
-// lane: 4096x11008 INT4 7.44 -> 6.93 us, INT8 10.48 -> 9.88 us) and the
-// 512-thread grid fills the CUs in whole rounds (a multiple of kCus
-// workgroups) or runs many (8+) of them.  A partial round among few costs
+// with one row per lane, INT8 with 8+ chunks per lane: 4096x11008 INT4
+// 7.44 -> 6.93 us, INT8 10.48 -> 9.88 us) and the 512-thread grid fills the
+// CUs in whole rounds (a multiple of kCus workgroups) or runs many (8+) of
+// them.  A partial round among few costs
 // more than the staging saves: 5120x13824 (640 workgroups of 512, 2.5
 // rounds; 1280 of 256) INT4 10.2 us with 512 threads, 9.8 with 256, INT8
 // 15.4 and 14.6; 5120^2 INT4 5.15 and 4.8.  Among many rounds the partial
@@ -1320,7 +1338,11 @@ bool rounds_ok_512(int64_t waves) {
 
 int lds_threads(bool int4, int r, int j, int64_t waves) {
     const bool rounds_ok = rounds_ok_512(waves);
-    if (int4 && (r == 2 || j >= 3) && rounds_ok) return 512;
+    // INT4: 512 threads with one row per lane (4096^2 3.38 us against 3.43,
+    // 4096x11008 6.82 against 7.14, 8192^2 8.19 against 8.48); with two
+    // rows 256 threads (11008x4096 6.05 against 6.14, 13824x5120 9.32
+    // against 10.30)
+    if (int4 && r == 1 && rounds_ok) return 512;
     if (!int4 && j >= 8 && rounds_ok) return 512;
     return kBlock;
 }
@@ -1726,6 +1748,24 @@ hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,
     return launch(stream_read_kernel, grid, kBlock, 0, stream, nullptr,
                   nullptr, static_cast<const uint4*>(buf),
                   static_cast<uint32_t*>(sink), n16, 0x9E3779B9u);
+}
+
+hipError_t launch_delay(double us, hipStream_t stream) {
+    if (!(us > 0.0)) return hipSuccess;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int khz = 0;   // wall clock rate in kHz (100 MHz on MI355X)
+    e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess) return e;
+    if (khz <= 0) return hipErrorInvalidValue;
+    const double t = us * static_cast<double>(khz) / 1000.0;
+    if (t > 1e12) return hipErrorInvalidValue;
+    const uint64_t ticks = static_cast<uint64_t>(t) + 1;
+    // each pass sleeps 8 x 64 cycles, several ticks: ticks + 1024 passes
+    // always outlast the wait and bound it if the clock were stuck
+    return launch(delay_kernel, 1, 64, 0, stream, nullptr, nullptr, ticks,
+                  ticks + 1024);
 }
 
 hipError_t launch_empty(int64_t grid, int block, void* sink,

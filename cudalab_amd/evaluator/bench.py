@@ -15,10 +15,12 @@ What is MI355X-specific:
 
 * Caliber.  A timed sample is `batch` back-to-back launches between two
   HIP events.  With caliber "native" (the default here) the launches come
-  from the library's C loop over the pool (cq_pool_timing); with "api"
-  they go through the Python extension object as in the reference.  The
-  GEMVs take 3-5 us on MI355X, less than one Python-boundary call, so the
-  "api" caliber times the host, not the kernels.
+  from the library's C loop over the pool (cq_pool_timing), queued behind
+  an on-device wait so that the host is ahead of the GPU for the whole
+  sample; with "api" they go through the Python extension object as in
+  the reference.  The GEMVs take 3-5 us on MI355X, less than one
+  Python-boundary call, so the "api" caliber times the host, not the
+  kernels.
 * Cache.  "streaming" pools are HBM-cold: distinct full (W, scale, x, out)
   sets totalling more than 512 MiB, twice the 256 MiB MALL, rotated launch
   by launch (the reference rotated only x/out over a shared W, which stays
@@ -119,8 +121,12 @@ def _api_sampler(pool: BenchPool, ext, variant: str):
 def _native_sampler(pool: BenchPool, variant: str):
     """k launches from the library's C loop (cq_pool_timing) over the
     pool's sets, continuing the rotation between calls; returns window us
-    (events on the current stream around the k launches)."""
-    from ..ext import pool_timing
+    (events on the current stream around the k launches).  A timed sample
+    is queued behind an on-device wait, so that the host has enqueued all k
+    launches before the GPU reaches them and the sample times the GPU, not
+    the host's submission rate (2.5-3.5 us per launch, as long as a short
+    GEMV)."""
+    from ..ext import pool_timing, prefill_delay_us
     if not pool.sets or not pool.op:
         raise ValueError("the native caliber needs a pool with sets and op")
     sets = pool.sets
@@ -131,7 +137,8 @@ def _native_sampler(pool: BenchPool, variant: str):
         o = off[0]
         rot = sets[o:] + sets[:o]
         r = pool_timing(pool.op, variant, rot, warmup=0, n_launches=k,
-                        per_kernel=False)
+                        per_kernel=False,
+                        delay_us=prefill_delay_us(k) if timed else 0.0)
         off[0] = (o + k) % n
         return r["total_us"]
     return run

@@ -4,7 +4,9 @@ Three reports, all printed to stdout:
 
   trace    per-kernel dispatch durations from a `--kernel-trace --stats` run
            (count, mean, median, min, max, and the median gap between
-           consecutive dispatches of the same kernel)
+           consecutive dispatches of the same kernel); optionally the
+           matched kernel's figures as JSON for bench.py's
+           `rocprof_us_per_dispatch` field
   counters per-dispatch medians of every counter in one or more `--pmc`
            runs, for the kernels matching each --match string
   traffic  HBM bytes per dispatch of one kernel from two `--pmc` runs
@@ -18,7 +20,7 @@ Reads rocprofv3's CSV output (`-f csv`: *_kernel_trace.csv,
 
 Usage:
   python -m cudalab_amd.evaluator.rocprof_summary trace DIR [--match S]
-      [--top N] [--by-grid]
+      [--top N] [--by-grid] [--shape N K --json-out FILE]
   python -m cudalab_amd.evaluator.rocprof_summary counters DIR [DIR ...]
       --match S [--match S ...]
   python -m cudalab_amd.evaluator.rocprof_summary traffic --fetch DIR
@@ -189,6 +191,18 @@ def report_trace(d: Path, match: str | None, top: int = 8,
     return "\n".join(lines)
 
 
+def trace_record(d: Path, match: str) -> dict:
+    """The dispatch-duration figures of the kernel matching `match` (the
+    one with the most dispatches)."""
+    by = dispatch_times(d)
+    name, v = _pick(by, match)
+    st = _stats_us([e - s for s, e in v])
+    gaps = sorted(v[i + 1][0] - v[i][1] for i in range(len(v) - 1)) or [0]
+    return {"kernel": name, "dispatches": st["n"], "mean_us": st["mean"],
+            "median_us": st["median"], "min_us": st["min"], "max_us": st["max"],
+            "gap_median_us": gaps[len(gaps) // 2] / 1e3}
+
+
 def report_traffic(fetch: Path, write: Path, match: str, calib_match: str,
                    calib_bytes: int) -> tuple[str, dict]:
     calib_kib = calib_bytes / 1024.0
@@ -245,6 +259,9 @@ def main(argv=None) -> int:
     t.add_argument("--top", type=int, default=8)
     t.add_argument("--by-grid", action="store_true",
                    help="one line per (kernel, grid size)")
+    t.add_argument("--shape", type=int, nargs=2, default=None)
+    t.add_argument("--json-out", type=Path, default=None,
+                   help="write the --match kernel's figures (and --shape) as JSON")
     c = sub.add_parser("counters")
     c.add_argument("dirs", type=Path, nargs="+")
     c.add_argument("--match", action="append", required=True)
@@ -260,6 +277,13 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         print(report_trace(a.dir, a.match, a.top, a.by_grid))
+        if a.json_out:
+            if not a.match:
+                raise SystemExit("--json-out needs --match")
+            rec = trace_record(a.dir, a.match)
+            rec["shape"] = list(a.shape) if a.shape else None
+            rec["kernel_match"] = a.match
+            a.json_out.write_text(json.dumps(rec, indent=1) + "\n")
         return 0
     if a.cmd == "counters":
         print(report_counters(a.dirs, a.match))

@@ -4,9 +4,11 @@ generations INT4, INT8 and FP16 over the reference's five bench shapes
 (cudalab/operators/int4gemv.py:30-36 lists the same matrix) in streaming
 (HBM-cold pool) and hot (one resident set) modes.
 
-Timing caliber: K back-to-back launches on one stream between two HIP
-events (cq_pool_timing), the same as bench.py's headline.  The read
-ceiling is cq_read_ceiling over an equally cold pool of the same bytes.
+Timing caliber: the same as bench.py's headline -- untimed launches for at
+least 100 ms, then K back-to-back launches on one stream between two HIP
+events, queued behind an on-device wait so that the window times the GPU
+and not the host's submission (cq_pool_timing).  The read ceiling is
+cq_read_ceiling over an equally cold pool of the same bytes, same caliber.
 
 Usage: python -m cudalab_amd.evaluator.sweep [--steps K] [--json FILE]
            [--ops int4gemv,qgemv,gemv] [--modes streaming,hot]
@@ -22,7 +24,7 @@ import sys
 
 import torch
 
-from ..ext import pool_timing, read_ceiling
+from ..ext import pool_timing, prefill_delay_us, read_ceiling
 from ..build import build
 from .bench import cold_pool_sets
 
@@ -62,7 +64,8 @@ def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
 def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
     torch.cuda.synchronize()
     r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
-                    per_kernel=False)
+                    per_kernel=False, burn_ms=100.0,
+                    delay_us=prefill_delay_us(steps))
     torch.cuda.synchronize()
     return r["total_us"] / steps
 
@@ -79,7 +82,8 @@ def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
            "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
            "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r", "tile", "block", "grid")}}
     if mode == "streaming":
-        c = read_ceiling(nbytes, warmup=warmup, n_launches=steps)
+        c = read_ceiling(nbytes, warmup=warmup, n_launches=steps, burn_ms=100.0,
+                         delay_us=prefill_delay_us(steps))
         rec["ceiling_us"] = round(c["us_per_call"], 4)
         rec["frac_ceiling"] = round(c["us_per_call"] / us, 4)
     del sets

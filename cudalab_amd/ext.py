@@ -563,15 +563,28 @@ def get_ext(op: str) -> _OpExt:
     return e
 
 
+def prefill_delay_us(n_launches: int) -> float:
+    """On-device wait to queue ahead of a window of `n_launches` launches so
+    that the host has enqueued all of them before the GPU reaches the first:
+    5 us per launch (host submission takes about 2.5-3.5 us per launch on
+    MI355X) plus 0.5 ms, at most 1 s."""
+    return float(min(1e6, 500.0 + 5.0 * n_launches))
+
+
 def pool_timing(op: str, variant: str, sets: list, warmup: int,
                 n_launches: int, per_kernel: bool,
-                stream: Optional[torch.cuda.Stream] = None) -> dict:
+                stream: Optional[torch.cuda.Stream] = None,
+                burn_ms: float = 0.0, delay_us: float = 0.0) -> dict:
     """Rotating-pool launch loop in native code (cq_pool_timing).
 
     `sets` is a list of (W, scale, x, out) tuples of one shape ((W, x, out)
-    for "gemv"), already validated by the caller.  Returns {"total_us":
-    window event time, "kernel_us": per-launch device durations (list) or
-    None}."""
+    for "gemv"), already validated by the caller.  Untimed launches run
+    until both `warmup` launches and `burn_ms` of wall-clock time have
+    passed; `delay_us` > 0 queues an on-device wait before the start event
+    so the host enqueues the window ahead of the GPU (see
+    prefill_delay_us).  Returns {"total_us": window event time,
+    "host_us": host time spent enqueuing the window, "kernel_us":
+    per-launch device durations (list) or None}."""
     lib = _capi.load()
     n = len(sets)
     VP = ctypes.c_void_p * n
@@ -589,20 +602,23 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
         op_id = GemvExt._op_id(W0)
     ku = (ctypes.c_float * n_launches)() if per_kernel else None
     tot = ctypes.c_double(0.0)
+    host = ctypes.c_double(0.0)
     dev = W0.device
     with torch.cuda.device(dev):
         s = stream if stream is not None else torch.cuda.current_stream(dev)
         st = lib.cq_pool_timing(
             op_id, variant.encode(), w, sc, xs, ys, n, N, K,
-            s.cuda_stream, warmup, n_launches, ku, ctypes.byref(tot))
+            s.cuda_stream, warmup, float(burn_ms), float(delay_us),
+            n_launches, ku, ctypes.byref(tot), ctypes.byref(host))
     if st != _capi.CQ_OK:
         _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")
-    return {"total_us": tot.value,
+    return {"total_us": tot.value, "host_us": host.value,
             "kernel_us": [float(v) for v in ku] if ku is not None else None}
 
 
 def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
-                 pool_bytes: int = 512 << 20, device: str = "cuda") -> dict:
+                 pool_bytes: int = 512 << 20, device: str = "cuda",
+                 burn_ms: float = 0.0, delay_us: float = 0.0) -> dict:
     """Bandwidth ceiling of one launch reading `nbytes`: a plain streaming
     read kernel (cq_read_ceiling) over a rotating pool of distinct buffers
     totalling more than `pool_bytes` (HBM-cold), timed like pool_timing."""
@@ -619,7 +635,8 @@ def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
     with torch.cuda.device(dev):
         s = torch.cuda.current_stream(dev)
         st = lib.cq_read_ceiling(arr, n, nbytes, sink.data_ptr(), s.cuda_stream,
-                                 warmup, n_launches, ctypes.byref(tot))
+                                 warmup, float(burn_ms), float(delay_us),
+                                 n_launches, ctypes.byref(tot))
     if st != _capi.CQ_OK:
         _fail(f"read_ceiling failed (status {st}): {_capi.last_error()}")
     us = tot.value / n_launches
@@ -628,7 +645,8 @@ def read_ceiling(nbytes: int, warmup: int = 200, n_launches: int = 2000,
 
 
 def launch_floor(grid: int, block: int, warmup: int = 200,
-                 n_launches: int = 2000, device: str = "cuda") -> float:
+                 n_launches: int = 2000, device: str = "cuda",
+                 burn_ms: float = 0.0, delay_us: float = 0.0) -> float:
     """µs per launch of a kernel with no memory work, `grid` workgroups of
     `block` threads, back to back on the current stream (cq_launch_floor):
     the per-dispatch cost of that launch shape in the pool-timing caliber."""
@@ -638,7 +656,8 @@ def launch_floor(grid: int, block: int, warmup: int = 200,
     with torch.cuda.device(sink.device):
         s = torch.cuda.current_stream(sink.device)
         st = lib.cq_launch_floor(int(grid), int(block), sink.data_ptr(),
-                                 s.cuda_stream, warmup, n_launches,
+                                 s.cuda_stream, warmup, float(burn_ms),
+                                 float(delay_us), n_launches,
                                  ctypes.byref(tot))
     if st != _capi.CQ_OK:
         _fail(f"launch_floor failed (status {st}): {_capi.last_error()}")

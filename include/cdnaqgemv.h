@@ -220,11 +220,27 @@ int cq_native_timing(int op, const char* variant, const void* w,
                      double* window_us, cq_timing_t* out);
 
 /*
+ * The timing loops below share one window.  Untimed launches run first,
+ * until both `warmup` launches and `burn_ms` milliseconds of wall-clock
+ * time have passed (clocks and power settle; the reference's measure_block
+ * burns at least 150 launches and 300 ms, cudalab/evaluator/bench.py:294-300),
+ * and the stream is synchronized.  Then, if delay_us > 0, a bounded
+ * on-device wait of about delay_us microseconds is queued (one wave, no
+ * memory work, bounded by an iteration count as well as by the clock), so
+ * that the host can enqueue the timed launches before the GPU reaches
+ * them; then the start event, the `n_launches` timed launches and the stop
+ * event.  *total_us receives the event time of the window.  The wait lies
+ * before the start event, outside the window.  Each call synchronizes the
+ * stream.  burn_ms must lie in [0, 600000] and delay_us in [0, 1e6].
+ */
+
+/*
  * Rotating-pool timing for HBM-cold ("streaming") measurement: launch i
- * (0 <= i < warmup + n_launches) uses set (i % n_sets) of the caller's
- * arrays w[], scale[], x[], y[].  *total_us receives the event time of
- * the timed window (two events around n_launches back-to-back launches).
- * If kernel_us (caller-owned, length n_launches) is non-NULL, every timed
+ * uses set (i % n_sets) of the caller's arrays w[], scale[], x[], y[]
+ * (the rotation runs on through warm-up and window).  *host_us (may be
+ * NULL) receives the host time spent enqueuing the window: when it reaches
+ * *total_us the window was bound by submission, not by the GPU.  If
+ * kernel_us (caller-owned, length n_launches) is non-NULL, every timed
  * launch also carries start/stop events on the dispatch itself
  * (hipExtLaunchKernel) and kernel_us[i] receives their difference; on
  * MI355X these per-dispatch events read about 4 us even for an empty
@@ -232,40 +248,37 @@ int cq_native_timing(int op, const char* variant, const void* w,
  * the reference's C++ layer: it restates the x/out rotation of
  * `BenchPool` + `measure_block`
  * (cudalab/evaluator/bench.py:197-309) in native code, with W rotated too.
- * Synchronizes the stream.
  */
 int cq_pool_timing(int op, const char* variant, const void* const* w,
                    const void* const* scale, const void* const* x,
                    void* const* y, int64_t n_sets, int64_t n, int64_t k,
-                   void* stream, int64_t warmup, int64_t n_launches,
-                   float* kernel_us, double* total_us);
+                   void* stream, int64_t warmup, double burn_ms,
+                   double delay_us, int64_t n_launches, float* kernel_us,
+                   double* total_us, double* host_us);
 
 /*
- * Read-only ceiling: `n_launches` back-to-back launches of a plain
- * streaming-read kernel, launch i reading `bytes` (a multiple of 16) from
- * bufs[i % n_bufs] (16-byte aligned device buffers), after `warmup`
- * untimed launches; *total_us receives the event time of the timed window.
- * `sink` is a device buffer of at least 4 bytes that the kernel may write.
- * No counterpart in the reference: it measures the bandwidth one launch
- * can reach for a given byte count on this device (the ceiling a GEMV call
- * of the same bytes is compared against).  Synchronizes the stream.
+ * Read-only ceiling: a plain streaming-read kernel, launch i reading
+ * `bytes` (a multiple of 16) from bufs[i % n_bufs] (16-byte aligned device
+ * buffers), in the window described above.  `sink` is a device buffer of
+ * at least 4 bytes that the kernel may write.  No counterpart in the
+ * reference: it measures the bandwidth one launch can reach for a given
+ * byte count on this device (the ceiling a GEMV call of the same bytes is
+ * compared against).
  */
 int cq_read_ceiling(const void* const* bufs, int64_t n_bufs, int64_t bytes,
-                    void* sink, void* stream, int64_t warmup,
-                    int64_t n_launches, double* total_us);
+                    void* sink, void* stream, int64_t warmup, double burn_ms,
+                    double delay_us, int64_t n_launches, double* total_us);
 
 /*
- * Launch floor: `n_launches` back-to-back launches of a kernel that does no
- * memory work, `grid` workgroups (1..INT_MAX) of `block` threads (1..1024),
- * after `warmup` untimed launches; *total_us receives the event time of the
- * timed window.  `sink` is a device buffer of at least 4 bytes (never
- * written).  No counterpart in the reference: it measures what one dispatch
- * of a GEMV's launch shape costs on this device before any kernel body
- * runs, the part of a call's time that no kernel change can remove.
- * Synchronizes the stream.
+ * Launch floor: a kernel that does no memory work, `grid` workgroups
+ * (1..INT_MAX) of `block` threads (1..1024), in the window described
+ * above.  `sink` is a device buffer of at least 4 bytes (never written).
+ * No counterpart in the reference: it measures what one dispatch of a
+ * GEMV's launch shape costs on this device before any kernel body runs.
  */
 int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
-                    int64_t warmup, int64_t n_launches, double* total_us);
+                    int64_t warmup, double burn_ms, double delay_us,
+                    int64_t n_launches, double* total_us);
 
 /*
  * Variant names of `op`, sorted, '\n'-separated, NUL-terminated, written to

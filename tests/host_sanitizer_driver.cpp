@@ -47,10 +47,13 @@ int main() {
     // timing argument errors
     cq_timing_t t; double tot;
     cq_native_timing(CQ_OP_INT4GEMV, "int4gemv_cdna4", P, P, P, Y, 8, 128, nullptr, -1, 1, 1, nullptr, &t);
-    cq_pool_timing(CQ_OP_INT4GEMV, "int4gemv_cdna4", nullptr, nullptr, nullptr, nullptr, 1, 8, 128, nullptr, 0, 1, nullptr, &tot);
+    cq_pool_timing(CQ_OP_INT4GEMV, "int4gemv_cdna4", nullptr, nullptr, nullptr, nullptr, 1, 8, 128, nullptr, 0, 0.0, 0.0, 1, nullptr, &tot, nullptr);
+    const void* one[1] = {P};
+    cq_pool_timing(CQ_OP_INT4GEMV, "int4gemv_cdna4", one, one, one, (void* const*)one, 1, 8, 128, nullptr, 0, -1.0, 0.0, 1, nullptr, &tot, nullptr);
     const void* bufs[2] = {(const void*)0x1000, (const void*)0x2008};
-    cq_read_ceiling(bufs, 2, 4096, Y, nullptr, 0, 1, &tot);
-    cq_launch_floor(0, 256, Y, nullptr, 0, 1, &tot);
+    cq_read_ceiling(bufs, 2, 4096, Y, nullptr, 0, 0.0, 0.0, 1, &tot);
+    cq_launch_floor(0, 256, Y, nullptr, 0, 0.0, 0.0, 1, &tot);
+    cq_launch_floor(256, 256, Y, nullptr, 0, 0.0, 1e7, 1, &tot);
     // describe, every op and size class
     for (int op : {CQ_OP_INT4GEMV, CQ_OP_QGEMV, CQ_OP_GEMV_F16, CQ_OP_GEMV_F32})
         for (int64_t n : {1, 7, 4096, 8192, 1 << 20})

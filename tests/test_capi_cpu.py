@@ -77,25 +77,30 @@ def test_vector_contract_predicate():
 
 
 @pytest.mark.parametrize("n,k,kernel,cw,j,r,block", [
-    (4096, 4096, "lds", 64, 2, 2, 512),      # 256 workgroups: whole rounds
-    (8192, 4096, "lds", 64, 2, 2, 512),      # 512
-    (11008, 4096, "lds", 64, 2, 1, 256),     # 688 would leave a partial round
-    (6144, 4096, "lds", 64, 2, 1, 256),      # 384: one row is 1.10x faster
-    (4096, 11008, "lds", 64, 6, 1, 512),      # 3+ chunks per lane: 512 threads
+    # up to 3 chunks per lane: one row per lane while one row per wave keeps
+    # the grid resident (n <= 32 waves x 256 CUs), 512 threads when their
+    # workgroups fill the CUs in whole rounds (or 8+ rounds)
+    (4096, 4096, "lds", 64, 2, 1, 512),      # 512 workgroups: whole rounds
+    (8192, 4096, "lds", 64, 2, 1, 512),      # 8192 rows: still resident
+    (6144, 4096, "lds", 64, 2, 1, 512),      # 768 workgroups: whole rounds
+    (3000, 4096, "lds", 64, 2, 1, 256),      # 375 would leave a partial round
     (1024, 4096, "lds", 64, 2, 1, 256),
-    (4096, 1024, "lds", 32, 1, 1, 256),
-    (1, 128, "lds", 16, 1, 1, 256),
+    # past 8192 rows one row per wave would run a second round of waves: two
+    # rows per lane, on 256-thread workgroups
+    (11008, 4096, "lds", 64, 2, 2, 256),
+    (8193, 4096, "lds", 64, 2, 2, 256),
+    (27648, 5120, "lds", 64, 3, 2, 256),
+    # rows of at most 32 chunks (several rows per wave): two rows per lane
+    (4096, 1024, "lds", 32, 1, 2, 256),
+    (1, 128, "lds", 16, 1, 2, 256),
+    (4096, 11008, "lds", 64, 6, 1, 512),
     (5, 16384, "lds", 64, 8, 1, 256),
-    # two rows per lane would leave fewer than 2048 waves
-    (3000, 4096, "lds", 64, 2, 1, 256),
-    # 4 chunks per lane (k = 8192): one row per lane at any n
+    # 4+ chunks per lane (k >= 8192): one row per lane at any n
     (8192, 8192, "lds", 64, 4, 1, 512),
     (57344, 8192, "lds", 64, 4, 1, 512),
     (4096, 6144, "lds", 64, 3, 1, 512),
-    # 512 threads only for whole rounds of 256 workgroups, or 8+ rounds
     (5120, 5120, "lds", 64, 3, 1, 256),      # 640: 2.5 rounds
     (5120, 13824, "lds", 64, 7, 1, 256),
-    (27648, 5120, "lds", 64, 3, 1, 512),     # 3456: 13.5 rounds
 ])
 def test_int4_launch_plans(n, k, kernel, cw, j, r, block):
     d = _capi.describe_launch("int4gemv", "int4gemv_cdna4", n, k, 4096, 8192)
@@ -247,25 +252,32 @@ def test_argument_errors_without_launch():
                               -1, 1, 1, None, ctypes.byref(t))
     assert st == _capi.CQ_ERR_INVALID_ARG and "warmup" in _capi.last_error()
     st = lib.cq_pool_timing(0, b"int4gemv_cdna4", None, None, None, None, 1,
-                            4, 128, None, 0, 1, None, None)
+                            4, 128, None, 0, 0.0, 0.0, 1, None, None, None)
     assert st == _capi.CQ_ERR_INVALID_ARG
+    one = (ctypes.c_void_p * 1)(0x1000)
+    for burn, delay, what in ((-1.0, 0.0, "burn_ms"), (float("nan"), 0.0, "burn_ms"),
+                              (1e9, 0.0, "burn_ms"), (0.0, -1.0, "delay_us"),
+                              (0.0, 2e6, "delay_us"), (0.0, float("inf"), "delay_us")):
+        st = lib.cq_pool_timing(0, b"int4gemv_cdna4", one, one, one, one, 1,
+                                4, 128, None, 0, burn, delay, 1, None, None, None)
+        assert st == _capi.CQ_ERR_INVALID_ARG and what in _capi.last_error()
     tot = ctypes.c_double()
     bufs = (ctypes.c_void_p * 2)(0x1000, 0x2008)
-    st = lib.cq_read_ceiling(bufs, 2, 4096, P, None, 0, 1, ctypes.byref(tot))
+    st = lib.cq_read_ceiling(bufs, 2, 4096, P, None, 0, 0.0, 0.0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "aligned" in _capi.last_error()
     bufs = (ctypes.c_void_p * 1)(0x1000)
-    st = lib.cq_read_ceiling(bufs, 1, 4100, P, None, 0, 1, ctypes.byref(tot))
+    st = lib.cq_read_ceiling(bufs, 1, 4100, P, None, 0, 0.0, 0.0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "multiple of 16" in _capi.last_error()
-    st = lib.cq_read_ceiling(bufs, 1, 4096, P, None, 0, 0, ctypes.byref(tot))
+    st = lib.cq_read_ceiling(bufs, 1, 4096, P, None, 0, 0.0, 0.0, 0, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG
-    st = lib.cq_read_ceiling(bufs, 1, 4096, None, None, 0, 1, ctypes.byref(tot))
+    st = lib.cq_read_ceiling(bufs, 1, 4096, None, None, 0, 0.0, 0.0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()
-    st = lib.cq_launch_floor(256, 512, None, None, 0, 1, ctypes.byref(tot))
+    st = lib.cq_launch_floor(256, 512, None, None, 0, 0.0, 0.0, 1, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "null" in _capi.last_error()
-    st = lib.cq_launch_floor(256, 512, P, None, 0, 0, ctypes.byref(tot))
+    st = lib.cq_launch_floor(256, 512, P, None, 0, 0.0, 0.0, 0, ctypes.byref(tot))
     assert st == _capi.CQ_ERR_INVALID_ARG and "n_launches" in _capi.last_error()
     for grid, block in ((0, 256), (1 << 31, 256), (256, 0), (256, 1025)):
-        st = lib.cq_launch_floor(grid, block, P, None, 0, 1, ctypes.byref(tot))
+        st = lib.cq_launch_floor(grid, block, P, None, 0, 0.0, 0.0, 1, ctypes.byref(tot))
         assert st == _capi.CQ_ERR_INVALID_ARG and "grid must be" in _capi.last_error()
 
 
