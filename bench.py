@@ -438,7 +438,9 @@ def main(argv=None) -> int:
     traffic = load_traffic(N, K)
     rp_us, rp_src = load_rocprof(N, K, args.mode, plan)
 
-    detail = {"plan": plan, "kernel_instance": kernel_instance(plan),
+    from cudalab_amd import _capi
+    detail = {"library": _capi.load().cq_version().decode(),
+              "plan": plan, "kernel_instance": kernel_instance(plan),
               "pool_sets": len(sets), "pool_bytes": len(sets) * nbytes,
               "algorithmic_bytes_per_call": nbytes,
               "window": {"launches": args.steps, "warmup_launches_min": args.warmup,

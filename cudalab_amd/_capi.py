@@ -15,7 +15,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-from .build import LIB_PATH
+from .build import LIB_PATH, source_hash
 
 CQ_OK = 0
 CQ_ERR_UNKNOWN_VARIANT = 1
@@ -35,6 +35,9 @@ CQ_DTYPE_F32 = 1
 # (torch on a GPU)
 CQ_SCALE_DIV = 0
 CQ_SCALE_RCP = 1
+
+# rows longer than this run the K-tiled kernels (cq_internal.h kMaxWaveK)
+MAX_UNTILED_K = 16384
 
 CQ_LIST_NORMAL = 0
 CQ_LIST_ALL = 1
@@ -124,6 +127,10 @@ class LibraryMissing(RuntimeError):
     pass
 
 
+class StaleLibrary(RuntimeError):
+    """The built library's source stamp differs from the tree's sources."""
+
+
 def lib_path() -> Path:
     return LIB_PATH
 
@@ -147,8 +154,22 @@ def load():
             fn = getattr(lib, name)  # AttributeError if not exported
             fn.restype = res
             fn.argtypes = args
+        built = library_stamp(lib)
+        tree = source_hash()
+        if built != tree:
+            raise StaleLibrary(
+                f"{LIB_PATH} was built from other sources than the tree holds "
+                f"(library src={built}, tree src={tree}); rebuild it with "
+                "`python -m cudalab_amd.build` (or __graft_entry__.build()).")
         _lib = lib
         return lib
+
+
+def library_stamp(lib) -> str:
+    """The source stamp compiled into a loaded library ("src=..." at the
+    end of cq_version())."""
+    v = lib.cq_version().decode("ascii", "replace")
+    return v.rsplit("src=", 1)[1] if "src=" in v else "unstamped"
 
 
 def last_error() -> str:

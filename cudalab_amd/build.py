@@ -27,6 +27,7 @@ does not preload.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -55,6 +56,22 @@ HIPCC_FLAGS = (
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
 )
+
+
+def source_hash() -> str:
+    """Stamp of what the library is built from: SHA-256 (first 16 hex
+    digits) over the compile flags and the names and bytes of every file
+    under cudalab_amd/csrc and include/.  Compiled into the library (its
+    cq_version() string ends in "src=<stamp>") and compared on load, so a
+    library built from other sources than the tree holds is refused."""
+    h = hashlib.sha256()
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    files = sorted(p for d in (CSRC, INCLUDE) for p in d.iterdir()
+                   if p.is_file() and p.suffix in (".hip", ".cpp", ".h"))
+    for p in files:
+        h.update(b"\0" + p.name.encode() + b"\0")
+        h.update(p.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def hipcc() -> str:
@@ -90,11 +107,12 @@ def build_library(verbose: bool = False) -> Path:
     with tempfile.TemporaryDirectory(prefix="cq_build_", dir=LIB_DIR) as tmp:
         objs = []
         cmds = []
+        stamp = f"-DCQ_SRC_HASH=\"{source_hash()}\""
         for src in SOURCES:
             obj = Path(tmp) / (Path(src).stem + ".o")
             objs.append(str(obj))
-            cmds.append([cc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c",
-                         str(CSRC / src), "-o", str(obj)])
+            cmds.append([cc, *HIPCC_FLAGS, stamp, f"-I{INCLUDE}", f"-I{CSRC}",
+                         "-c", str(CSRC / src), "-o", str(obj)])
         with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
             for f in [ex.submit(_run, c) for c in cmds]:
                 f.result()

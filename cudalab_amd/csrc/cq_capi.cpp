@@ -724,6 +724,11 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
 
 const char* cq_last_error(void) { return g_last_error.c_str(); }
 
-const char* cq_version(void) { return "cdnaqgemv 0.1.0 (gfx950)"; }
+// The build passes CQ_SRC_HASH, a stamp of the sources and flags the
+// library was compiled from; the Python loader compares it with the tree.
+#ifndef CQ_SRC_HASH
+#define CQ_SRC_HASH "unstamped"
+#endif
+const char* cq_version(void) { return "cdnaqgemv 0.2.0 (gfx950) src=" CQ_SRC_HASH; }
 
 }  // extern "C"

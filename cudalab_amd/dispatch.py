@@ -8,12 +8,15 @@ Two tables behind one module:
   working (cudalab/dispatch.py:44-137, tests/test_dispatch.py).  That table
   routes the reference's RMSNorm variants; the RMSNorm kernels themselves
   are outside this build's path, the table is data.
-* The quantized GEMV table of this build: `select_gemv_variant(op, N, K)`
+* The quantized GEMV routing of this build: `select_gemv_variant(op, N, K)`
   and `gemv_dispatch_info(op, N, K)`.  Policy as in the reference's GEMV
   reports (one incumbent for every shape, report v0.7 section 11 Q6): the
-  CDNA4 wave kernel, which itself takes the scalar path when the vector
-  contract is unmet or K exceeds its register-resident x (then
-  evidence_source says so).
+  `*_cdna4` variant.  What that variant runs for a given call is the
+  library's own launch plan (cq_describe_launch), so the answer names the
+  kernel that actually runs: the LDS kernel; the K-tiled LDS kernel for
+  rows longer than 16384 elements or weights of 4 GiB or more; or the
+  scalar kernel when the vector contract is unmet (bit-identical to the
+  baseline variant), with the library's reason.
 """
 from __future__ import annotations
 
@@ -116,7 +119,9 @@ def dispatch_info(M: int, H: int, dtype: torch.dtype = torch.float16) -> dict:
 
 GEMV_INCUMBENT = {"int4gemv": "int4gemv_cdna4", "qgemv": "qgemv_cdna4"}
 GEMV_BASELINE = {"int4gemv": "int4gemv_baseline", "qgemv": "qgemv_baseline"}
-MAX_WAVE_K = 16384   # wave kernels keep x in registers up to this K
+# stand-in device addresses for a plan query: only their 16-byte alignment
+# matters to the planner, nothing is read or launched
+_ALIGNED_W, _ALIGNED_X = 1 << 12, 1 << 13
 
 
 def select_gemv_variant(op: str, N: int, K: int) -> str:
@@ -130,20 +135,36 @@ def select_gemv_variant(op: str, N: int, K: int) -> str:
     return GEMV_INCUMBENT[op]
 
 
-def gemv_dispatch_info(op: str, N: int, K: int) -> dict:
+def gemv_dispatch_info(op: str, N: int, K: int, w_offset: int = 0,
+                       x_offset: int = 0) -> dict:
+    """Routing of a quantized GEMV call: the variant, and the kernel and
+    launch shape the library plans for it.  `w_offset` / `x_offset` are the
+    byte misalignments of W and x from a 16-byte boundary (0: aligned).
+    evidence_source is "incumbent" when the vectorized kernels run and
+    "scalar-path" when the plan falls back to the scalar kernel."""
+    from . import _capi
     v = select_gemv_variant(op, N, K)
-    granule = 32 if op == "int4gemv" else 16
-    if K > MAX_WAVE_K:
-        source, why = ("scalar-path",
-                       f"K={K} > {MAX_WAVE_K}: the incumbent runs its scalar "
-                       "kernel (bit-identical to the baseline variant)")
-    elif K % granule != 0:
-        source, why = ("scalar-path",
-                       f"K % {granule} != 0: vector contract unmet, scalar "
-                       "kernel")
+    d = _capi.describe_launch(op, v, N, K, _ALIGNED_W + int(w_offset),
+                              _ALIGNED_X + int(x_offset))
+    plan = {key: int(d[key]) for key in ("cw", "j", "r", "tile", "block", "grid")}
+    kernel = d["kernel"]
+    if kernel == "scalar":
+        source = "scalar-path"
+        why = (f"{d['why']}: scalar kernel, bit-identical to "
+               f"{GEMV_BASELINE[op]}")
+    elif kernel == "tiled":
+        source = "incumbent"
+        cause = (f"K={K} > {_capi.MAX_UNTILED_K}" if K > _capi.MAX_UNTILED_K
+                 else "weights of 4 GiB or more (64-bit row bases)")
+        why = (f"K-tiled LDS kernel ({cause}): x staged in LDS "
+               f"{plan['tile']} chunks per lane at a time, {plan['r']} "
+               f"row(s) per wave, {plan['block']}-thread workgroups")
     else:
-        source, why = ("incumbent",
-                       "CDNA4 wave kernel for every shape (vectorized when "
-                       "W and x are 16-byte aligned)")
-    return {"op": op, "N": N, "K": K, "variant": v,
+        source = "incumbent"
+        why = (f"LDS kernel: x staged once per workgroup in LDS, "
+               f"{plan['r']} row(s) per lane, {plan['cw']} lanes per row, "
+               f"{plan['j']} chunk(s) per lane, {plan['block']}-thread "
+               "workgroups")
+    return {"op": op, "N": N, "K": K, "variant": v, "kernel": kernel,
+            "plan": plan, "fallback": d["fallback"] == "1",
             "evidence_source": source, "reason": why}

@@ -1,37 +1,42 @@
-"""Round-level paired statistics of the A/B methodology (pure CPU: no GPU,
-no torch).
+"""Statistics of the paired A/B methodology (pure CPU: no GPU, no torch).
 
-Restates `cudalab/evaluator/stats.py` (harness paired-streaming-v2.3):
+What a decision rests on (the policy of the reference's harness
+paired-streaming-v2.3, cudalab/evaluator/stats.py:1-222; the thresholds,
+record keys and reason key words are kept so that records and callers stay
+comparable, the code is this build's own):
 
-* The unit of inference is the independent benchmark *round*, never the
-  individual timed sample: within a round the two variants are measured
-  back to back on the same tensors, and only round-level speedups
-  (parent / candidate, > 1 means the candidate is faster) enter the
-  statistics (:1-12, :170-199).
-* Percentile bootstrap of the median round speedup with a fixed seed, so a
-  record's CI is reproducible bit for bit (:202-222).  The resampling order
-  (Python `random.Random(seed).randrange(n)`, n draws per replicate) and
-  the percentile indices are kept exactly as the reference's, so the same
-  speedups give the same interval.
-* Symmetric guards (:26-143): a timed sample farther than a factor 1.5
-  from the median of the last 50 accepted samples is rejected (fast and
-  slow alike); a block whose filtered median is farther than 1.15 from the
-  running median of that variant's earlier blocks invalidates the round
-  (after 3 warm-up blocks).  Every block keeps raw and filtered statistics.
-* Filter sensitivity (:146-167): raw and filtered speedups that fall on
-  opposite sides of 1.0, or differ by more than 10% (|log ratio| >
-  log 1.10), mark the record as filter-sensitive.
-* The clock-agreement checks (:225-258) of the v0.2 harness, kept for old
-  records (no timed round samples clocks any more).
+* Rounds, not samples.  Within a round the two variants are timed back to
+  back on the same pool; a round contributes one speedup, parent /
+  candidate (> 1: the candidate is faster).  Samples only feed the round's
+  medians.
+* Two guards, both symmetric (a sample or block that is too fast is as
+  suspect as one that is too slow):
+    - a timed sample outside [m / 1.5, m * 1.5], m the median of the last
+      50 samples the guard accepted in the same block, is rejected;
+    - a block whose filtered median lies outside [r / 1.15, r * 1.15], r
+      the median of the same variant's earlier block medians, flags its
+      round (once 3 earlier blocks exist).
+  Both bounds are inclusive: a value exactly on a bound is accepted.  Every
+  block keeps the raw and the filtered track, so a record can show what the
+  guards changed (`filter_sensitive`).
+* A fixed-seed percentile bootstrap of the median round speedup, so that a
+  record's interval reproduces bit for bit: replicate b draws n indices with
+  `random.Random(seed).randrange(n)` in sequence, and the bounds are the
+  sorted replicates at int(alpha/2 * B) and int((1 - alpha/2) * B) - 1 (the
+  reference's draw order and indices, so the same speedups give the same
+  interval).
 
-Reason strings carry the reference's key words (方向翻转 / 阈值内 / 未评估)
-next to the English text, because callers match them.
+GPU clocks are not sampled inside a round on MI355X (amd-smi snapshots are
+taken before and after a run, evaluator/gpu.py), so there is no clock
+agreement check here.
 """
 from __future__ import annotations
 
 import math
 import random
 import statistics
+from collections import Counter, deque
+from typing import Iterable, Optional
 
 BOOTSTRAP_SEED = 20260919
 BOOTSTRAP_N = 10000
@@ -45,179 +50,174 @@ CROSSBLOCK_FACTOR = 1.15
 CROSSBLOCK_WARMUP = 3
 
 
+def _side(value: float, center: float, factor: float) -> Optional[str]:
+    """Which side of the band [center / factor, center * factor] `value`
+    falls out of: "slow" above, "fast" below, None inside (bounds
+    included)."""
+    if value > center * factor:
+        return "slow"
+    if value < center / factor:
+        return "fast"
+    return None
+
+
 # ------------------------------------------------------------ sample guard
+class SampleGuard:
+    """The sample-level guard of one block.  Samples are offered in timing
+    order; each is judged against the median of the last `window` samples
+    this guard accepted (the first sample is always accepted)."""
+
+    def __init__(self, factor: float = SPIKE_FACTOR,
+                 window: int = SPIKE_WINDOW) -> None:
+        self.factor = factor
+        self._recent: deque[float] = deque(maxlen=window)
+        self.accepted: list[float] = []
+        self.rejected: Counter[str] = Counter()
+
+    def verdict(self, t_us: float) -> Optional[str]:
+        """"fast" / "slow" if `t_us` would be rejected, else None (the
+        guard's state is not changed)."""
+        if not self._recent:
+            return None
+        return _side(t_us, statistics.median(self._recent), self.factor)
+
+    def offer(self, t_us: float) -> Optional[str]:
+        """Judge one sample and record it; returns the rejection side or
+        None when accepted."""
+        side = self.verdict(t_us)
+        if side is None:
+            self._recent.append(t_us)
+            self.accepted.append(t_us)
+        else:
+            self.rejected[side] += 1
+        return side
+
+
 def apply_spike_guard(accepted: list[float], t_us: float,
                       spike_factor: float = SPIKE_FACTOR,
-                      window: int = SPIKE_WINDOW) -> tuple[bool, str | None]:
-    """Accept or reject one timed sample against the median of the last
-    `window` accepted samples: (False, "slow") above ref * factor, (False,
-    "fast") below ref / factor, else (True, None).  The thresholds are
-    strict (a sample exactly at a threshold is accepted) and the first
-    sample of a block is always accepted."""
-    if not accepted:
-        return True, None
-    ref = statistics.median(accepted[-window:])
-    if t_us > ref * spike_factor:
-        return False, "slow"
-    if t_us < ref / spike_factor:
-        return False, "fast"
-    return True, None
+                      window: int = SPIKE_WINDOW) -> tuple[bool, Optional[str]]:
+    """Stateless form of the sample guard: (accepted?, side) of `t_us`
+    against the median of the last `window` entries of `accepted`."""
+    side = (None if not accepted else
+            _side(t_us, statistics.median(accepted[-window:]), spike_factor))
+    return side is None, side
 
 
-def block_stats(raw_samples_us: list[float],
+def block_stats(raw_samples_us: Iterable[float],
                 spike_factor: float = SPIKE_FACTOR,
                 window: int = SPIKE_WINDOW) -> dict:
-    """Raw and filtered statistics of one block of timed samples (the guard
-    applied sample by sample, in order)."""
-    kept: list[float] = []
-    fast = slow = 0
-    for t in raw_samples_us:
-        ok, why = apply_spike_guard(kept, t, spike_factor, window)
-        if ok:
-            kept.append(t)
-        elif why == "fast":
-            fast += 1
-        else:
-            slow += 1
+    """Raw and filtered tracks of one block of timed samples."""
+    raw = list(raw_samples_us)
+    guard = SampleGuard(spike_factor, window)
+    for t in raw:
+        guard.offer(t)
+    kept = guard.accepted
+    n_out = guard.rejected["fast"] + guard.rejected["slow"]
     return {
         "median_us": statistics.median(kept) if kept else None,
-        "raw_median_us": (statistics.median(raw_samples_us)
-                          if raw_samples_us else None),
-        "n_raw": len(raw_samples_us),
+        "raw_median_us": statistics.median(raw) if raw else None,
+        "n_raw": len(raw),
         "n_accepted": len(kept),
-        "n_rejected_fast": fast,
-        "n_rejected_slow": slow,
-        # field names older records used for the same counts
+        "n_rejected_fast": guard.rejected["fast"],
+        "n_rejected_slow": guard.rejected["slow"],
+        # the same counts under the field names of older records
         "n_clean": len(kept),
-        "n_spike": fast + slow,
-        "raw_samples_us": [round(t, 3) for t in raw_samples_us],
+        "n_spike": n_out,
+        "raw_samples_us": [round(t, 3) for t in raw],
         "accepted_samples_us": [round(t, 3) for t in kept],
     }
 
 
-def crossblock_flag(hist: list[float], med: float | None,
+# ------------------------------------------------------------- block guard
+def crossblock_flag(hist: list[float], med: Optional[float],
                     factor: float = CROSSBLOCK_FACTOR,
                     warmup: int = CROSSBLOCK_WARMUP) -> dict:
-    """Judge one block's filtered median `med` against the running median
-    of the same variant's earlier blocks (`hist`, owned by the caller; med
-    is appended after judging, warm-up blocks included).  Flags "slow"
-    above median * factor and "fast" below median / factor once at least
-    `warmup` blocks are in hist.  med None is neither judged nor
-    appended."""
-    info: dict = {"running_med_us": None, "ratio": None,
-                  "flagged": False, "direction": None}
+    """Judge a block's filtered median `med` against the median of the same
+    variant's earlier block medians `hist` (a list the caller keeps per
+    variant; `med` is appended after it is judged, so warm-up blocks enter
+    the history too).  Nothing is judged before `warmup` earlier blocks
+    exist, and a missing median is neither judged nor recorded."""
+    out: dict = {"running_med_us": None, "ratio": None, "flagged": False,
+                 "direction": None}
     if med is None:
-        return info
+        return out
     if len(hist) >= warmup:
-        running = statistics.median(hist)
-        ratio = med / running if running > 0 else float("inf")
-        info["running_med_us"] = round(running, 3)
-        info["ratio"] = round(ratio, 4)
-        if ratio > factor:
-            info["flagged"], info["direction"] = True, "slow"
-        elif ratio < 1.0 / factor:
-            info["flagged"], info["direction"] = True, "fast"
+        ref = statistics.median(hist)
+        ratio = med / ref if ref > 0 else math.inf
+        side = _side(ratio, 1.0, factor)
+        out.update(running_med_us=round(ref, 3), ratio=round(ratio, 4),
+                   flagged=side is not None, direction=side)
     hist.append(med)
-    return info
+    return out
 
 
-def filter_sensitive(raw_speedup: float | None,
-                     filtered_speedup: float | None,
+def filter_sensitive(raw_speedup: Optional[float],
+                     filtered_speedup: Optional[float],
                      log_delta: float = FILTER_LOG_DELTA) -> tuple[bool, str]:
-    """Whether the guards changed the conclusion: the raw and filtered
-    paired speedups lie strictly on opposite sides of 1.0, or
-    |log(filtered / raw)| > log_delta.  Missing or non-positive inputs are
-    not evaluated (False)."""
-    if (raw_speedup is None or filtered_speedup is None
-            or raw_speedup <= 0 or filtered_speedup <= 0):
-        return False, "not evaluated (未评估): raw or filtered speedup missing or invalid"
-    if (raw_speedup < 1.0 < filtered_speedup
-            or filtered_speedup < 1.0 < raw_speedup):
+    """Did the guards change the conclusion?  Yes when the raw and the
+    filtered paired speedups lie strictly on opposite sides of 1.0, or their
+    ratio is beyond exp(log_delta) either way.  A missing or non-positive
+    speedup is not evaluated."""
+    if not (raw_speedup and filtered_speedup
+            and raw_speedup > 0 and filtered_speedup > 0):
+        return False, ("not evaluated (未评估): raw or filtered speedup "
+                       "missing or invalid")
+    if (raw_speedup - 1.0) * (filtered_speedup - 1.0) < 0:
         return True, (f"direction flip (方向翻转): raw {raw_speedup:.4f} and "
-                      f"filtered {filtered_speedup:.4f} lie on opposite sides of 1.0")
-    delta = abs(math.log(filtered_speedup / raw_speedup))
-    if delta > log_delta:
-        return True, (f"|log(filtered/raw)| = {delta:.4f} > {log_delta:.4f} "
-                      f"(more than 10% apart)")
-    return False, (f"within threshold (阈值内): |log difference| {delta:.4f} "
+                      f"filtered {filtered_speedup:.4f} lie on opposite "
+                      "sides of 1.0")
+    gap = abs(math.log(filtered_speedup) - math.log(raw_speedup))
+    if gap > log_delta:
+        return True, (f"|log(filtered/raw)| = {gap:.4f} > {log_delta:.4f} "
+                      "(more than 10% apart)")
+    return False, (f"within threshold (阈值内): |log difference| {gap:.4f} "
                    f"<= {log_delta:.4f}")
 
 
 # --------------------------------------------------------- round statistics
 def paired_speedups(parent_round_us: list[float],
                     candidate_round_us: list[float]) -> list[float]:
-    """Per-round parent / candidate (> 1 = candidate faster).  The lists
-    are the two variants' medians of the same rounds."""
+    """Per-round parent / candidate from the two variants' round medians."""
     if len(parent_round_us) != len(candidate_round_us):
         raise ValueError(f"paired lengths differ: {len(parent_round_us)} vs "
                          f"{len(candidate_round_us)}")
-    out = []
-    for p, c in zip(parent_round_us, candidate_round_us):
-        if p <= 0 or c <= 0:
-            raise ValueError(f"non-positive time: parent={p} candidate={c}")
-        out.append(p / c)
-    return out
+    bad = [(p, c) for p, c in zip(parent_round_us, candidate_round_us)
+           if p <= 0 or c <= 0]
+    if bad:
+        p, c = bad[0]
+        raise ValueError(f"non-positive time: parent={p} candidate={c}")
+    return [p / c for p, c in zip(parent_round_us, candidate_round_us)]
+
+
+_SUMMARY_KEYS = ("n", "median", "mean", "min", "max", "faster_count",
+                 "faster_fraction")
 
 
 def summarize(speedups: list[float]) -> dict:
+    """Count, centre, spread and the share of rounds the candidate won."""
     if not speedups:
-        return {"n": 0, "median": None, "mean": None, "min": None,
-                "max": None, "faster_count": 0, "faster_fraction": None}
-    faster = sum(1 for s in speedups if s > 1.0)
-    return {
-        "n": len(speedups),
-        "median": round(statistics.median(speedups), 6),
-        "mean": round(statistics.fmean(speedups), 6),
-        "min": round(min(speedups), 6),
-        "max": round(max(speedups), 6),
-        "faster_count": faster,
-        "faster_fraction": round(faster / len(speedups), 4),
-    }
+        return dict.fromkeys(_SUMMARY_KEYS) | {"n": 0, "faster_count": 0}
+    wins = sum(s > 1.0 for s in speedups)
+    r6 = lambda v: round(v, 6)  # noqa: E731
+    return {"n": len(speedups), "median": r6(statistics.median(speedups)),
+            "mean": r6(statistics.fmean(speedups)), "min": r6(min(speedups)),
+            "max": r6(max(speedups)), "faster_count": wins,
+            "faster_fraction": round(wins / len(speedups), 4)}
 
 
 def bootstrap_ci(values: list[float], statistic: str = "median",
                  n_boot: int = BOOTSTRAP_N, alpha: float = CI_ALPHA,
-                 seed: int = BOOTSTRAP_SEED) -> list[float] | None:
-    """Percentile bootstrap CI [lo, hi] of the median (or mean) of
-    `values`; None for fewer than 3 values."""
+                 seed: int = BOOTSTRAP_SEED) -> Optional[list[float]]:
+    """Percentile bootstrap interval [lo, hi] of the median (or "mean") of
+    `values`, or None for fewer than 3 values (draw order in the module
+    docstring)."""
     n = len(values)
     if n < 3:
         return None
-    rng = random.Random(seed)
     stat = statistics.median if statistic == "median" else statistics.fmean
-    reps = []
-    for _ in range(n_boot):
-        reps.append(stat([values[rng.randrange(n)] for _ in range(n)]))
-    reps.sort()
+    draw = random.Random(seed).randrange
+    reps = sorted(stat([values[draw(n)] for _ in range(n)])
+                  for _ in range(n_boot))
     lo = reps[int((alpha / 2) * n_boot)]
     hi = reps[int((1.0 - alpha / 2) * n_boot) - 1]
     return [round(lo, 6), round(hi, 6)]
-
-
-# ------------------------------------------------ clock agreement (v0.2)
-def check_dvfs_pair(clk_before, clk_after_first, clk_after_second,
-                    parent_first: bool, tol: float) -> tuple:
-    """A paired round's clock agreement: each variant's effective clock is
-    the mean of the samples around its measurement; a relative difference
-    above `tol` invalidates the round.  Returns (valid, reason,
-    eff_parent, eff_candidate)."""
-    if not (clk_before and clk_after_first and clk_after_second):
-        return False, "no_clock_data", None, None
-    first = (clk_before + clk_after_first) / 2.0
-    second = (clk_after_first + clk_after_second) / 2.0
-    eff_p, eff_c = (first, second) if parent_first else (second, first)
-    mid = (eff_p + eff_c) / 2.0
-    ok = abs(eff_p - eff_c) / mid <= tol if mid > 0 else False
-    return ok, (None if ok else "INVALID_DVFS"), eff_p, eff_c
-
-
-def check_dvfs_matrix(clks: list, tol: float) -> tuple:
-    """A matrix round's clock agreement: the spread of the variants'
-    effective clocks (means of adjacent samples) over their mean must not
-    exceed `tol`.  Returns (valid, reason, effective_clocks)."""
-    if not clks or not all(clks):
-        return False, "no_clock_data", []
-    effs = [(clks[i] + clks[i + 1]) / 2.0 for i in range(len(clks) - 1)]
-    spread = (max(effs) - min(effs)) / statistics.fmean(effs)
-    ok = spread <= tol
-    return ok, (None if ok else "INVALID_DVFS"), effs

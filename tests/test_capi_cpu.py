@@ -415,3 +415,21 @@ def test_gemv_argument_errors_without_launch():
         _capi.variant_list("gemv_f16", _capi.CQ_LIST_ALL)
     assert _capi.vec_contract_ok("gemv_f32", 0x1000, 0x2000, 12)
     assert not _capi.vec_contract_ok("gemv_f16", 0x1000, 0x2000, 12)
+
+
+def test_library_carries_the_source_stamp_of_the_tree():
+    from cudalab_amd.build import source_hash
+    lib = _capi.load()
+    v = lib.cq_version().decode()
+    assert v.startswith("cdnaqgemv ") and "(gfx950)" in v
+    assert _capi.library_stamp(lib) == source_hash()
+    assert len(source_hash()) == 16
+
+
+def test_stale_library_is_refused(monkeypatch):
+    """A library whose stamp differs from the tree's sources does not load."""
+    _capi.load()
+    monkeypatch.setattr(_capi, "_lib", None)
+    monkeypatch.setattr(_capi, "source_hash", lambda: "0123456789abcdef")
+    with pytest.raises(_capi.StaleLibrary, match="other sources"):
+        _capi.load()

@@ -75,15 +75,47 @@ def test_gemv_routing(op):
         info = dispatch.gemv_dispatch_info(op, N, K)
         assert info["variant"] == f"{op}_cdna4"
         assert info["evidence_source"] == "incumbent"
+        assert info["kernel"] == "lds" and not info["fallback"]
+        assert "LDS kernel" in info["reason"]
+    # past 16384 elements per row the incumbent runs the K-tiled kernel
     info = dispatch.gemv_dispatch_info(op, 8, 16512)
-    assert info["evidence_source"] == "scalar-path"
+    assert info["evidence_source"] == "incumbent"
+    assert info["kernel"] == "tiled" and "K-tiled" in info["reason"]
+    assert "16512 > 16384" in info["reason"]
     with pytest.raises(KeyError):
         dispatch.select_gemv_variant("gemv", 1, 1)
     with pytest.raises(ValueError):
         dispatch.select_gemv_variant(op, 0, 128)
 
 
+@pytest.mark.parametrize("op", ["int4gemv", "qgemv"])
+@pytest.mark.parametrize("N,K,woff,xoff", [
+    (4096, 4096, 0, 0), (11008, 4096, 0, 0), (8, 16512, 0, 0),
+    (8192, 28672, 0, 0), (4096, 4096, 2, 0), (4096, 4096, 0, 2),
+    (1 << 20, 8192, 0, 0),
+])
+def test_gemv_routing_agrees_with_the_library_plan(op, N, K, woff, xoff):
+    """The routing answer is the plan the library launches for that call."""
+    from cudalab_amd import _capi
+    info = dispatch.gemv_dispatch_info(op, N, K, woff, xoff)
+    d = _capi.describe_launch(op, f"{op}_cdna4", N, K, 4096 + woff, 8192 + xoff)
+    assert info["kernel"] == d["kernel"]
+    assert info["plan"] == {k: int(d[k]) for k in ("cw", "j", "r", "tile", "block", "grid")}
+    assert info["fallback"] == (d["fallback"] == "1")
+    assert (info["evidence_source"] == "scalar-path") == (d["kernel"] == "scalar")
+    if woff or xoff:
+        assert info["kernel"] == "scalar" and "alignment" in info["reason"]
+        assert f"{op}_baseline" in info["reason"]
+    if N == 1 << 20:    # 4 GiB of weights or more: tiled, 64-bit row bases
+        big = N * (K // 2 if op == "int4gemv" else K) >= 1 << 32
+        assert info["kernel"] == ("tiled" if big else "lds")
+        if big:
+            assert "4 GiB" in info["reason"]
+
+
 def test_gemv_routing_int4_k_contract():
     with pytest.raises(ValueError):
         dispatch.select_gemv_variant("int4gemv", 8, 100)
-    assert dispatch.gemv_dispatch_info("qgemv", 8, 13)["evidence_source"] == "scalar-path"
+    info = dispatch.gemv_dispatch_info("qgemv", 8, 13)
+    assert info["evidence_source"] == "scalar-path" and info["kernel"] == "scalar"
+    assert "k%16" in info["reason"]

@@ -6,6 +6,7 @@ same inputs must give the same verdicts."""
 from __future__ import annotations
 
 import math
+import random
 import statistics
 
 import pytest
@@ -72,19 +73,30 @@ def test_bootstrap_matches_an_independent_restatement():
         [round(reps[250], 6), round(reps[9749], 6)]
 
 
-def test_dvfs_checks():
-    ok, why, _, _ = S.check_dvfs_pair(1350, 1905, 1905, parent_first=True, tol=0.05)
-    assert not ok and why == "INVALID_DVFS"
-    ok, why, ep, ec = S.check_dvfs_pair(1900, 1905, 1902, parent_first=True, tol=0.05)
-    assert ok and why is None and abs(ep - 1902.5) < 1e-9 and abs(ec - 1903.5) < 1e-9
-    ok, why, ep, ec = S.check_dvfs_pair(1900, 1905, 1902, parent_first=False, tol=0.05)
-    assert abs(ep - 1903.5) < 1e-9 and abs(ec - 1902.5) < 1e-9
-    assert S.check_dvfs_pair(None, 1900, 1900, True, 0.05)[:2] == (False, "no_clock_data")
-    ok, _, effs = S.check_dvfs_matrix([1900, 1905, 1902, 1898, 1901, 1904], tol=0.05)
-    assert ok and len(effs) == 5
-    assert S.check_dvfs_matrix([1350, 1350, 1350, 1905, 1905, 1905], 0.05)[:2] == \
-        (False, "INVALID_DVFS")
-    assert S.check_dvfs_matrix([1900, None, 1900], 0.05)[:2] == (False, "no_clock_data")
+def test_sample_guard_matches_the_stateless_guard():
+    """The block tracker and the one-sample function judge alike: random
+    sample streams with spikes both ways, fed sample by sample."""
+    rng = random.Random(3)
+    for trial in range(200):
+        kept, sides = [], []
+        guard = S.SampleGuard()
+        for i in range(rng.randint(1, 160)):
+            t = rng.uniform(9.0, 11.0) * rng.choice([1, 1, 1, 1.6, 1 / 1.6, 1.49])
+            ok, side = S.apply_spike_guard(kept, t)
+            assert guard.verdict(t) == side
+            assert guard.offer(t) == side
+            if ok:
+                kept.append(t)
+            else:
+                sides.append(side)
+        assert guard.accepted == kept
+        assert guard.rejected["fast"] == sides.count("fast")
+        assert guard.rejected["slow"] == sides.count("slow")
+
+
+def test_clock_agreement_helpers_are_gone():
+    """MI355X rounds sample no clocks: no clock-agreement helper remains."""
+    assert not hasattr(S, "check_dvfs_pair") and not hasattr(S, "check_dvfs_matrix")
 
 
 # ---------------------------------------------------- decision rules (v0.2)
@@ -397,3 +409,43 @@ def test_bench_matrix_rotates_and_classifies(monkeypatch):
     assert (cell["winner"], cell["runner_up"]) == ("b", "a")
     assert cell["status"] == E.SIGNIFICANT_WINNER
     B.bench_matrix(_FakeOp(), _FakeExt(), ["alias_of_a", "b"], 1, 1, rounds=1)
+
+
+# ------------------------------------------------------ negative-case runner
+def test_negative_runner_records_and_pass_rule():
+    from cudalab_amd.evaluator import negative as N
+
+    def boom(msg):
+        def f():
+            raise RuntimeError(msg + "\nsecond line")
+        return f
+
+    ok = lambda: True      # noqa: E731
+    bad = lambda: False    # noqa: E731
+    r = N.run_case("v", "d", boom("x 必须是 2 维"), "reject", "必须是 2 维", ok)
+    assert r["status"] == "rejected" and r["msg_match"] is True and r["pass"]
+    assert r["exception_type"] == "RuntimeError" and r["message"] == "x 必须是 2 维"
+    r = N.run_case("v", "d", boom("other"), "reject", "必须是 2 维", ok)
+    assert r["msg_match"] is False and not r["pass"]
+    r = N.run_case("v", "d", boom("anything"), "reject", None, ok)
+    assert r["msg_match"] is None and r["pass"]
+    r = N.run_case("v", "d", lambda: None, "reject", None, ok)
+    assert r["status"] == "passed_without_exception" and not r["pass"]
+    r = N.run_case("v", "d", lambda: None, "pass", None, ok)
+    assert r["pass"] and r["post_check_ok"] is True
+    r = N.run_case("v", "d", boom("x"), "pass", None, ok)
+    assert not r["pass"]
+    r = N.run_case("v", "d", boom("x 必须是 2 维"), "reject", "必须是 2 维", bad)
+    assert r["post_check_ok"] is False and not r["pass"]
+    r = N.run_case("v", "d", boom("y" * 400), "reject", None, ok)
+    assert len(r["message"]) == 300
+    s = N.run_case("v", "d", lambda: None, "skip", None, bad)
+    assert s["status"] == "skipped" and "pass" not in s and s["post_check_ok"] is None
+    recs = [N.run_case("v", "d", boom("m"), "reject", "m", ok),
+            N.run_case("v", "d", lambda: None, "reject", None, ok),
+            N.run_case("v", "d", lambda: None, "pass", None, ok), s]
+    summ = N.summarize_cases(recs)
+    assert summ == {"n_total": 4, "n_reject_expected": 2, "n_reject_ok": 1,
+                    "n_pass_expected": 1, "n_pass_ok": 1, "n_skipped": 1,
+                    "n_passed": 2, "all_pass": False}
+    assert N.summarize_cases(recs[:1] + recs[2:])["all_pass"]
