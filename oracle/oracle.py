@@ -26,6 +26,10 @@ the reference repository).  How each is pinned (tests/test_oracle_*.py):
                           planted mistakes (transposed W, dropped term,
                           fp16 accumulation) exceed it
   ulp32                   numpy.spacing on float32
+  expect_exact_*          the exact value cast once to the output type, for
+                          inputs whose every FP32 partial sum is exact in any
+                          order (conditions checked on entry); pinned against
+                          exact_* and Fraction sums (tests/test_exact_inputs_cpu.py)
 """
 from __future__ import annotations
 
@@ -390,3 +394,82 @@ def max_threads() -> int:
     if env and env.isdigit():
         return int(env)
     return int(lib().orc_max_threads())
+
+
+# ------------------------------------------- exact-input expectations
+#
+# For inputs built so that every FP32 partial sum of the products is exact
+# whatever the summation order, the only rounding left in any correct kernel
+# is the final cast of the exact value to the output type.  Its result is
+# then known bit for bit, at any K and for every variant (the fixed bound
+# above allows 6K roundings per term, so at large K it cannot see a dropped
+# chunk of work; this can).
+#
+# INT4: scales are powers of two in [2^-6, 2^-2], x in {-1, 0, +1}, and
+#   K <= 131072.  Every product q * s * x is a multiple of 2^-6 with
+#   |q * s| <= 2, so every partial sum is a multiple of 2^-6 of magnitude
+#   at most 2K <= 2^18: at most 2^24 units of 2^-6, exact in FP32.
+# INT8: scales are powers of two in [2^-8, 2^0] (one per row), x in
+#   {-1, 0, +1}, K <= 131072.  Per row the partial sums are s times an
+#   integer of magnitude at most 128K <= 2^24: exact, applied before or
+#   after the scale.
+# FP16/FP32: every W element is q * 2^-e with q an integer, |q| <= 8 and
+#   e in [2, 6], x in {-1, 0, +1}, K <= 131072: multiples of 2^-6 below
+#   2^18, as for INT4.
+
+EXACT_MAX_K = 131072
+
+
+def _pow2_exponents(v: np.ndarray) -> np.ndarray:
+    m, e = np.frexp(np.asarray(v, dtype=np.float64))
+    if np.any(m != 0.5):
+        raise ValueError("exact-input condition: every scale must be a power of two")
+    return e - 1
+
+
+def _unit_x(x: np.ndarray) -> None:
+    xf = np.asarray(x).astype(np.float64)
+    if not np.all(np.isin(xf, (-1.0, 0.0, 1.0))):
+        raise ValueError("exact-input condition: x must lie in {-1, 0, +1}")
+
+
+def expect_exact_w4(wp: np.ndarray, scale: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """fp16 of the exact INT4 GEMV for exact inputs (conditions above)."""
+    K = 2 * np.asarray(wp).shape[1]
+    if K > EXACT_MAX_K:
+        raise ValueError(f"exact-input condition: K = {K} > {EXACT_MAX_K}")
+    e = _pow2_exponents(np.asarray(scale, dtype=np.float16))
+    if e.size and (e.min() < -6 or e.max() > -2):
+        raise ValueError("exact-input condition: INT4 scales in [2^-6, 2^-2]")
+    _unit_x(x)
+    ex, _ = exact_w4(wp, scale, x)
+    return ex.astype(np.float16)
+
+
+def expect_exact_w8(wq: np.ndarray, scale: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """fp16 of the exact INT8 GEMV for exact inputs (conditions above)."""
+    K = np.asarray(wq).shape[1]
+    if K > EXACT_MAX_K:
+        raise ValueError(f"exact-input condition: K = {K} > {EXACT_MAX_K}")
+    e = _pow2_exponents(np.asarray(scale, dtype=np.float32))
+    if e.size and (e.min() < -8 or e.max() > 0):
+        raise ValueError("exact-input condition: INT8 scales in [2^-8, 1]")
+    _unit_x(x)
+    ex, _ = exact_w8(wq, scale, x)
+    return ex.astype(np.float16)
+
+
+def expect_exact_gemv(W: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """The exact FP16/FP32 GEMV cast to W's dtype, for exact inputs."""
+    W = np.asarray(W)
+    K = W.shape[1]
+    if K > EXACT_MAX_K:
+        raise ValueError(f"exact-input condition: K = {K} > {EXACT_MAX_K}")
+    w = W.astype(np.float64)
+    u = w * 64.0                              # in units of 2^-6
+    if np.any(u != np.round(u)) or np.any(np.abs(w) > 2.0):
+        raise ValueError("exact-input condition: W must be multiples of 2^-6 "
+                         "of magnitude at most 2")
+    _unit_x(x)
+    ex, _ = exact_gemv(W, np.asarray(x, dtype=W.dtype))
+    return ex.astype(W.dtype)

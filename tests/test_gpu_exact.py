@@ -1,0 +1,219 @@
+"""GPU parity on exact inputs: every variant of the three operators, bit for
+bit against the exact value cast once to the output type.
+
+Inputs are built so that every FP32 partial sum is exact in any summation
+order (oracle.expect_exact_*: random weight bytes, power-of-two scales,
+x in {-1, 0, +1}; FP16/FP32 weights that are multiples of 2^-6).  A correct
+kernel then has exactly one rounding, the final cast, so its output is
+known bit for bit at any K -- where the fixed accumulation bound (6K
+roundings per term) cannot see missing work.  Covered: the five bench
+shapes and edge shapes, K up to 131072 with partial last tiles, both sides
+of the K-tiled plans' 3072-row boundary, grouped calls (single, several and
+nine problems, long rows), misaligned operands (scalar fallback), and
+weights past 4 GiB (sampled rows).  The CPU side (test_exact_inputs_cpu.py)
+pins the expectation and shows that one dropped 16-byte chunk at
+K = 131072 fails this comparison while it passes the bound.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+INT4_SHAPES = [(1, 128), (3, 128), (16, 256), (65, 384), (300, 1280), (7, 16384),
+               (1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096), (4096, 11008),
+               (64, 16512), (300, 20480), (4097, 28672), (33, 65536), (2, 131072),
+               (3072, 28672), (3073, 28672)]
+Q8_SHAPES = [(1, 1), (16, 13), (8, 7), (17, 16), (300, 1040), (5, 16384),
+             (1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096), (4096, 11008),
+             (7, 16400), (64, 20480), (4097, 28672), (33, 65536), (2, 131072),
+             (3072, 28672), (3073, 28672)]
+GEMV_SHAPES = [(1, 1), (16, 13), (33, 1000), (1024, 4096), (4096, 1024), (4096, 4096),
+               (11008, 4096), (4096, 11008), (3, 16376), (2, 32768), (300, 40000),
+               (33, 65536), (2, 131072)]
+
+
+def _gen(seed):
+    return torch.Generator(device="cuda").manual_seed(seed)
+
+
+def _unit_x(K, g, dtype=torch.float16):
+    return torch.randint(-1, 2, (K,), device="cuda", generator=g).to(dtype)
+
+
+def _int4_exact(N, K, seed):
+    g = _gen(seed)
+    wp = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device="cuda", generator=g)
+    e = torch.randint(-6, -1, (N, K // 128), device="cuda", generator=g)
+    s = torch.pow(2.0, e.float()).half()
+    return wp, s, _unit_x(K, g)
+
+
+def _q8_exact(N, K, seed):
+    g = _gen(seed)
+    wq = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    s = torch.pow(2.0, torch.randint(-8, 1, (N,), device="cuda", generator=g).float())
+    return wq, s, _unit_x(K, g)
+
+
+def _gemv_exact(N, K, dtype, seed):
+    g = _gen(seed)
+    q = torch.randint(-8, 9, (N, K), device="cuda", generator=g).float()
+    e = torch.randint(2, 7, (N, K), device="cuda", generator=g).float()
+    W = (q * torch.pow(2.0, -e)).to(dtype)
+    return W, _unit_x(K, g, dtype)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _same_bits(y, want, what):
+    got = _np(y)
+    bits = np.uint16 if got.dtype == np.float16 else np.uint32
+    a, b = got.view(bits), np.ascontiguousarray(want).view(bits)
+    bad = np.flatnonzero(a != b)
+    assert bad.size == 0, (f"{what}: {bad.size} of {a.size} outputs differ from "
+                           f"the exact value (first rows {bad[:5].tolist()}: got "
+                           f"{got[bad[:3]].tolist()}, want {want[bad[:3]].tolist()})")
+
+
+@pytest.fixture(scope="module")
+def extg(cuda):
+    from cudalab_amd.build import build
+    return build("gemv")
+
+
+@pytest.mark.parametrize("N,K", INT4_SHAPES)
+def test_int4_every_variant_exact(ext4, N, K):
+    wp, s, x = _int4_exact(N, K, seed=N * 7 + K)
+    want = orc.expect_exact_w4(_np(wp), _np(s), _np(x))
+    for v in ext4.variants():
+        announce(f"int4gemv exact {v} N={N} K={K}")
+        y = ext4.forward(v, wp, s, x)
+        torch.cuda.synchronize()
+        _same_bits(y, want, f"{v} {N}x{K}")
+
+
+@pytest.mark.parametrize("N,K", Q8_SHAPES)
+def test_q8_every_variant_exact(ext8, N, K):
+    wq, s, x = _q8_exact(N, K, seed=N * 7 + K)
+    want = orc.expect_exact_w8(_np(wq), _np(s), _np(x))
+    for v in ext8.variants():
+        announce(f"qgemv exact {v} N={N} K={K}")
+        y = ext8.forward(v, wq, s, x)
+        torch.cuda.synchronize()
+        _same_bits(y, want, f"{v} {N}x{K}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+@pytest.mark.parametrize("N,K", GEMV_SHAPES)
+def test_gemv_every_variant_exact(extg, dtype, N, K):
+    W, x = _gemv_exact(N, K, dtype, seed=N * 7 + K)
+    want = orc.expect_exact_gemv(_np(W), _np(x))
+    for v in extg.variants():
+        announce(f"gemv exact {v} {dtype} N={N} K={K}")
+        y = extg.forward(v, W, x)
+        torch.cuda.synchronize()
+        _same_bits(y, want, f"{v} {dtype} {N}x{K}")
+
+
+def _misaligned(t, offset_bytes):
+    """Same values at a base pointer `offset_bytes` past a 16-byte boundary."""
+    n = t.numel() * t.element_size()
+    flat = torch.zeros(n + 64, dtype=torch.uint8, device=t.device)
+    view = flat[offset_bytes:offset_bytes + n].view(t.dtype).view_as(t)
+    view.copy_(t)
+    return view
+
+
+@pytest.mark.parametrize("woff,xoff", [(2, 0), (0, 2), (2, 2)])
+def test_misaligned_operands_exact(ext4, ext8, extg, woff, xoff):
+    """Operands off a 16-byte boundary take the scalar kernel; still exact."""
+    wp, s, x = _int4_exact(300, 4096, seed=1)
+    want = orc.expect_exact_w4(_np(wp), _np(s), _np(x))
+    wpm, xm = _misaligned(wp, woff), _misaligned(x, xoff)
+    assert ext4.describe("int4gemv_cdna4", wpm, xm)["kernel"] == "scalar"
+    announce(f"int4gemv exact misaligned w+{woff} x+{xoff}")
+    _same_bits(ext4.forward("int4gemv_cdna4", wpm, s, xm), want, "int4 misaligned")
+    wq, s8, x8 = _q8_exact(300, 4096, seed=2)
+    want8 = orc.expect_exact_w8(_np(wq), _np(s8), _np(x8))
+    announce(f"qgemv exact misaligned w+{woff} x+{xoff}")
+    _same_bits(ext8.forward("qgemv_cdna4", _misaligned(wq, woff), s8, _misaligned(x8, xoff)),
+               want8, "int8 misaligned")
+    W, xg = _gemv_exact(300, 4096, torch.float16, seed=3)
+    wantg = orc.expect_exact_gemv(_np(W), _np(xg))
+    announce(f"gemv exact misaligned w+{woff} x+{xoff}")
+    _same_bits(extg.forward("gemv_cdna4", _misaligned(W, woff), _misaligned(xg, xoff)),
+               wantg, "gemv misaligned")
+
+
+GROUPS = {
+    "qkv": ([(4096, 4096)] * 3, 4096),
+    "gate_up": ([(11008, 4096)] * 2, 4096),
+    "mixed": ([(1, 4096), (33, 4096), (4099, 4096), (300, 4096), (64, 4096)], 4096),
+    "nine": ([(128 + 16 * i, 1024) for i in range(9)], 1024),
+    "long_rows": ([(3072, 28672), (3073, 28672), (64, 28672)], 28672),
+    "k131072": ([(2, 131072), (3, 131072)], 131072),
+}
+
+
+@pytest.mark.parametrize("name", list(GROUPS))
+def test_grouped_calls_exact(ext4, ext8, name):
+    shapes, K = GROUPS[name]
+    for op, ext, make, expect, variants in (
+            ("int4gemv", ext4, _int4_exact, orc.expect_exact_w4,
+             ("int4gemv_cdna4", "int4gemv_lds_r1", "int4gemv_baseline")),
+            ("qgemv", ext8, _q8_exact, orc.expect_exact_w8,
+             ("qgemv_cdna4", "qgemv_lds_r1", "qgemv_baseline"))):
+        probs = [make(N, K, seed=100 * i + N) for i, (N, _) in enumerate(shapes)]
+        wants = [expect(_np(W), _np(s), _np(x)) for (W, s, x) in probs]
+        for v in variants:
+            announce(f"{op} grouped exact {name} {v}")
+            outs = [torch.full((W.size(0),), float("nan"), dtype=torch.float16,
+                               device="cuda") for (W, _, _) in probs]
+            ext.forward_grouped(v, [(W, s, x, o) for (W, s, x), o in zip(probs, outs)])
+            torch.cuda.synchronize()
+            for i, (o, want) in enumerate(zip(outs, wants)):
+                _same_bits(o, want, f"{op} {name} {v} problem {i}")
+
+
+@pytest.mark.parametrize("op", ["int4gemv", "qgemv", "gemv"])
+def test_weights_past_4gib_exact(op, ext4, ext8, extg):
+    """W just over 4 GiB (k = 8192): the incumbents plan the tiled kernel
+    with 64-bit row bases.  Rows on both sides of the 4 GiB byte mark and
+    the first and last rows must be exact (sampled: the matrix is not
+    copied to the host)."""
+    K = 8192
+    row_bytes = {"int4gemv": K // 2, "qgemv": K, "gemv": 2 * K}[op]
+    first_past = (1 << 32) // row_bytes
+    N = first_past + 3
+    announce(f"{op} exact weights past 4 GiB N={N} K={K}")
+    rows = torch.tensor([0, 1, N // 2, first_past - 2, first_past - 1, first_past,
+                         first_past + 1, N - 1], device="cuda")
+    if op == "int4gemv":
+        W, s, x = _int4_exact(N, K, seed=21)
+        want = orc.expect_exact_w4(_np(W[rows]), _np(s[rows]), _np(x))
+        ext, args, variants = ext4, (W, s, x), ("int4gemv_cdna4", "int4gemv_baseline")
+    elif op == "qgemv":
+        W, s, x = _q8_exact(N, K, seed=22)
+        want = orc.expect_exact_w8(_np(W[rows]), _np(s[rows]), _np(x))
+        ext, args, variants = ext8, (W, s, x), ("qgemv_cdna4", "qgemv_baseline")
+    else:
+        W, x = _gemv_exact(N, K, torch.float16, seed=23)
+        want = orc.expect_exact_gemv(_np(W[rows]), _np(x))
+        ext, args, variants = extg, (W, x), ("gemv_cdna4", "gemv_baseline")
+    assert W.numel() * W.element_size() > (1 << 32)
+    assert ext.describe(variants[0], W, x)["kernel"] == "tiled"
+    for v in variants:
+        announce(f"{op} exact weights past 4 GiB {v}")
+        y = ext.forward(v, *args)
+        torch.cuda.synchronize()
+        _same_bits(y[rows], want, f"{op} {v} past 4 GiB")
+    del W, args
+    torch.cuda.empty_cache()
