@@ -170,3 +170,58 @@ def test_one_dropped_chunk_at_k131072_fails_the_exact_check(op):
     # ... the exact comparison does, on nearly every row
     differ = int(np.count_nonzero(wrong.view(np.uint16) != want.view(np.uint16)))
     assert differ >= N - 1, differ
+
+
+# ------------------------------------------- the timed CPU baseline ports
+@pytest.mark.parametrize("threads", [1, 4])
+@pytest.mark.parametrize("N,K", [(1, 128), (37, 4096), (256, 1024), (5, 16512)])
+def test_cpu_port_w4_meets_the_bound_and_is_exact_on_exact_inputs(N, K, threads):
+    """orc_int4_gemv_cpu (the C + OpenMP GEMV bench.py times as the CPU
+    baseline) computes the same GEMV: within the bound on quantized N(0,1)
+    data in every input mode, bit for bit on exact inputs, and the same
+    bits for any thread count."""
+    rng = np.random.default_rng(N + K)
+    for mode_w, mode_x in ((0.02, 1.0), (1e-4, 1e-4), (10.0, 10.0)):
+        W = (rng.standard_normal((N, K)) * mode_w).astype(np.float16)
+        wp, s = orc.quantize_w4(W)
+        x = (rng.standard_normal(K) * mode_x).astype(np.float16)
+        y = orc.gemv_w4_cpu(wp, s, x, threads)
+        ex, S = orc.exact_w4(wp, s, x)
+        fits = np.abs(ex) <= 65504
+        assert orc.arith_ratio(y[fits], ex[fits], S[fits], K).max(initial=0) <= 1.0
+        assert np.array_equal(y.view(np.uint16), orc.gemv_w4_cpu(wp, s, x, 1).view(np.uint16))
+    wp, s, x = _w4_inputs(rng, N, K)
+    y = orc.gemv_w4_cpu(wp, s, x, threads)
+    assert np.array_equal(y.view(np.uint16), orc.expect_exact_w4(wp, s, x).view(np.uint16))
+
+
+@pytest.mark.parametrize("threads", [1, 4])
+@pytest.mark.parametrize("N,K", [(1, 1), (16, 13), (37, 4096), (5, 16400)])
+def test_cpu_port_w8_meets_the_bound_and_is_exact_on_exact_inputs(N, K, threads):
+    rng = np.random.default_rng(N + K)
+    for mode_w, mode_x in ((0.02, 1.0), (1e-4, 1e-4), (10.0, 10.0)):
+        W = (rng.standard_normal((N, K)) * mode_w).astype(np.float16)
+        wq, s = orc.quantize_w8(W)
+        x = (rng.standard_normal(K) * mode_x).astype(np.float16)
+        y = orc.gemv_w8_cpu(wq, s, x, threads)
+        ex, S = orc.exact_w8(wq, s, x)
+        fits = np.abs(ex) <= 65504
+        assert orc.arith_ratio(y[fits], ex[fits], S[fits], K).max(initial=0) <= 1.0
+        assert np.array_equal(y.view(np.uint16), orc.gemv_w8_cpu(wq, s, x, 1).view(np.uint16))
+    wq, s, x = _w8_inputs(rng, N, K)
+    y = orc.gemv_w8_cpu(wq, s, x, threads)
+    assert np.array_equal(y.view(np.uint16), orc.expect_exact_w8(wq, s, x).view(np.uint16))
+
+
+def test_cpu_port_rejects_a_planted_mistake():
+    """The check above is not vacuous: the port's output with one weight
+    byte changed fails the exact comparison."""
+    rng = np.random.default_rng(9)
+    wp, s, x = _w4_inputs(rng, 8, 4096)
+    s[:, 0] = np.float16(0.25)             # group 0 of every row: the largest scale
+    x[14] = np.float16(1.0)
+    bad = wp.copy()
+    bad[:, 7] ^= 0x01                      # element 14 of every row: q moves by 1
+    y = orc.gemv_w4_cpu(bad, s, x, 2)
+    want = orc.expect_exact_w4(wp, s, x)
+    assert np.count_nonzero(y.view(np.uint16) != want.view(np.uint16)) == 8

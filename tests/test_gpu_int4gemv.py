@@ -185,6 +185,38 @@ def test_product_suite_incumbent(ext4, tmp_path):
                                         out_dir=tmp_path)
     assert r["all_pass"], r["summary"]["failed"]
     assert r["summary"]["n_total"] == 50
+    _check_fidelity(tmp_path / "quantization_fidelity.json")
+
+
+# The reference's archived layer-(c) record for the same 5 shapes x 5 modes
+# (experiments/int4gemv/correctness/v0.7/quantization_fidelity.json:46-51):
+# min cosine 0.981436545655207, max step error 0.5053995847702026, max |q| 7.
+REF_MIN_COSINE = 0.981436545655207
+
+
+def _check_fidelity(path):
+    """Layer (c): quantization fidelity, asserted rather than only reported.
+    - max |q| is 7 (every non-zero group reaches the clamp);
+    - the dequant step error |W - q*s16| / s16 stays within what the
+      quantizer guarantees: |W - q*s32| <= s32/2 and |s16 - s32| <= d*s32
+      give (1/2 + 7d) / (1 - d), with d = 2^-11 for normal fp16 scales and
+      up to 2^-9 for the subnormal scales of the "tiny" mode (N(0, 1e-4)
+      weights: group scales >= 2^-16);
+    - the cosine of y_quant against y_orig is no worse than the reference's
+      archived minimum over the same matrix (its data came from the CUDA
+      generator, so only the floor carries over)."""
+    import json
+    d = json.loads(path.read_text())
+    summ, cases = d["summary"], d["cases"]
+    assert summ["n_cases"] == 25 and summ["max_abs_q"] == 7
+    for c in cases:
+        if c["mode"] == "zeros":
+            assert c["max_abs_q"] == 0 and c["cosine"] is None
+            continue
+        dd = 2.0 ** -9 if c["mode"] == "tiny" else 2.0 ** -11
+        assert c["max_abs_q"] == 7, c
+        assert c["max_dequant_step_err"] <= (0.5 + 7 * dd) / (1 - dd), c
+    assert summ["min_cosine"] >= REF_MIN_COSINE, summ
 
 
 def test_native_and_pool_timing(ext4):

@@ -139,3 +139,28 @@ def test_product_suite_incumbent(ext8, tmp_path):
     r = get("qgemv").run_correctness(ext8, "qgemv_cdna4", out_dir=tmp_path)
     assert r["all_pass"], r["summary"]["failed"]
     assert r["summary"]["n_total"] == 50
+    _check_fidelity(tmp_path / "quantization_fidelity.json")
+
+
+# The reference's archived layer-(c) record
+# (experiments/qgemv/correctness/v0.6/quantization_fidelity.json): min cosine
+# 0.9998970268657201, max step error 0.5000019073486328, max |q| 127.
+REF_MIN_COSINE = 0.9998970268657201
+
+
+def _check_fidelity(path):
+    """Layer (c) asserted: max |q| is 127; the step error |W - q*s| / s of
+    the fp32 per-row scale is 1/2 plus FP32 rounding of W/s and q*s (at most
+    128 * 2^-24 each way); the cosine is no worse than the reference's
+    archived minimum."""
+    import json
+    d = json.loads(path.read_text())
+    summ, cases = d["summary"], d["cases"]
+    assert summ["n_cases"] == 25 and summ["max_abs_q"] == 127
+    for c in cases:
+        if c["mode"] == "zeros":
+            assert c["max_abs_q"] == 0 and c["cosine"] is None
+            continue
+        assert c["max_abs_q"] == 127, c
+        assert c["max_dequant_step_err"] <= 0.5 + 2 * 128 * 2.0 ** -24, c
+    assert summ["min_cosine"] >= REF_MIN_COSINE, summ
