@@ -91,11 +91,15 @@ def parse_args(argv=None):
                          "(counter calibration runs)")
     ap.add_argument("--cpu-sweep", action="store_true",
                     help="time only the CPU paths at the five bench shapes")
+    ap.add_argument("--prefill-us", type=float, default=None,
+                    help="on-device wait queued before the headline window "
+                         "(default: 5 us per launch + 0.5 ms); profiling runs, "
+                         "whose host submission is slower, need more")
     return ap.parse_args(argv)
 
 
 def gpu_loop(op: str, variant: str, sets, steps: int, warmup: int,
-             burn_ms: float) -> dict:
+             burn_ms: float, delay_us: float | None = None) -> dict:
     """One window of `steps` back-to-back launches rotating through `sets`,
     pre-filled behind an on-device wait, timed by two HIP events around the
     window (native loop, no per-launch events)."""
@@ -105,7 +109,7 @@ def gpu_loop(op: str, variant: str, sets, steps: int, warmup: int,
     t0 = time.perf_counter()
     r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
                     per_kernel=False, burn_ms=burn_ms,
-                    delay_us=prefill_delay_us(steps))
+                    delay_us=prefill_delay_us(steps) if delay_us is None else delay_us)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     return {"total_us": r["total_us"], "us_per_call": r["total_us"] / steps,
@@ -430,7 +434,7 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
 
     r = gpu_loop("int4gemv", args.variant, sets, args.steps, args.warmup,
-                 args.burn_ms)
+                 args.burn_ms, args.prefill_us)
 
     total_s = r["total_us"] * 1e-6
     value = nbytes * args.steps / total_s / 1e9

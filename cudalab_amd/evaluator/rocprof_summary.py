@@ -20,7 +20,7 @@ Reads rocprofv3's CSV output (`-f csv`: *_kernel_trace.csv,
 
 Usage:
   python -m cudalab_amd.evaluator.rocprof_summary trace DIR [--match S]
-      [--top N] [--by-grid] [--shape N K --json-out FILE]
+      [--top N] [--by-grid] [--shape N K --json-out FILE [--after K2]]
   python -m cudalab_amd.evaluator.rocprof_summary counters DIR [DIR ...]
       --match S [--match S ...]
   python -m cudalab_amd.evaluator.rocprof_summary traffic --fetch DIR
@@ -191,16 +191,30 @@ def report_trace(d: Path, match: str | None, top: int = 8,
     return "\n".join(lines)
 
 
-def trace_record(d: Path, match: str) -> dict:
+def trace_record(d: Path, match: str, after: str | None = None) -> dict:
     """The dispatch-duration figures of the kernel matching `match` (the
-    one with the most dispatches)."""
+    one with the most dispatches).  With `after`, only its dispatches that
+    start after the end of the last dispatch of the kernel matching `after`
+    count (bench.py queues an on-device wait right before its timed window,
+    so `after="delay_kernel"` selects the window), and the record also gives
+    the window's start-to-start rate: (last end - first start) / n."""
     by = dispatch_times(d)
     name, v = _pick(by, match)
+    rec: dict = {"kernel": name}
+    if after:
+        _, marks = _pick(by, after)
+        t0 = marks[-1][1]
+        v = [(s, e) for s, e in v if s >= t0]
+        if not v:
+            raise SystemExit(f"no {match!r} dispatch after the last {after!r}")
+        rec["selected"] = f"dispatches after the last {after}"
+        rec["window_us_per_dispatch"] = (v[-1][1] - v[0][0]) / len(v) / 1e3
     st = _stats_us([e - s for s, e in v])
     gaps = sorted(v[i + 1][0] - v[i][1] for i in range(len(v) - 1)) or [0]
-    return {"kernel": name, "dispatches": st["n"], "mean_us": st["mean"],
-            "median_us": st["median"], "min_us": st["min"], "max_us": st["max"],
-            "gap_median_us": gaps[len(gaps) // 2] / 1e3}
+    rec.update({"dispatches": st["n"], "mean_us": st["mean"],
+                "median_us": st["median"], "min_us": st["min"], "max_us": st["max"],
+                "gap_median_us": gaps[len(gaps) // 2] / 1e3})
+    return rec
 
 
 def report_traffic(fetch: Path, write: Path, match: str, calib_match: str,
@@ -262,6 +276,8 @@ def main(argv=None) -> int:
     t.add_argument("--shape", type=int, nargs=2, default=None)
     t.add_argument("--json-out", type=Path, default=None,
                    help="write the --match kernel's figures (and --shape) as JSON")
+    t.add_argument("--after", default=None,
+                   help="JSON record: only dispatches after the last one of this kernel")
     c = sub.add_parser("counters")
     c.add_argument("dirs", type=Path, nargs="+")
     c.add_argument("--match", action="append", required=True)
@@ -280,7 +296,8 @@ def main(argv=None) -> int:
         if a.json_out:
             if not a.match:
                 raise SystemExit("--json-out needs --match")
-            rec = trace_record(a.dir, a.match)
+            rec = trace_record(a.dir, a.match, a.after)
+            print(json.dumps(rec, indent=1))
             rec["shape"] = list(a.shape) if a.shape else None
             rec["kernel_match"] = a.match
             a.json_out.write_text(json.dumps(rec, indent=1) + "\n")

@@ -71,7 +71,7 @@ def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
 
 
 def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
-            steps: int, warmup: int) -> dict:
+            steps: int, warmup: int, ceiling: bool = True) -> dict:
     sets, nbytes = make_sets(op, N, K, mode)
     x0 = sets[0][1] if op == "gemv" else sets[0][2]
     plan = ext.describe(variant, sets[0][0], x0)
@@ -81,7 +81,7 @@ def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
            "us_per_call": round(us, 4), "GBps": round(nbytes / us / 1e3, 1),
            "frac_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
            "plan": {k: plan[k] for k in ("kernel", "cw", "j", "r", "tile", "block", "grid")}}
-    if mode == "streaming":
+    if mode == "streaming" and ceiling:
         c = read_ceiling(nbytes, warmup=warmup, n_launches=steps, burn_ms=100.0,
                          delay_us=prefill_delay_us(steps))
         rec["ceiling_us"] = round(c["us_per_call"], 4)
@@ -93,16 +93,18 @@ def _record(op: str, ext, variant: str, N: int, K: int, mode: str,
 
 def run(ops=tuple(OPS), shapes=SHAPES, modes=("streaming", "hot"),
         steps: int = 2000, warmup: int = 200,
-        variants: dict | None = None) -> list[dict]:
+        variants: dict | None = None, ceiling: bool = True) -> list[dict]:
     """One record per (op, variant, shape, mode); `variants` maps an op to
-    the variants to time (default: its incumbent)."""
+    the variants to time (default: its incumbent); `ceiling` False skips
+    the read-ceiling measurement (profiling runs)."""
     out = []
     for op in ops:
         ext = build(op)
         for variant in (variants or {}).get(op, [OPS[op]]):
             for (N, K) in shapes:
                 for mode in modes:
-                    out.append(_record(op, ext, variant, N, K, mode, steps, warmup))
+                    out.append(_record(op, ext, variant, N, K, mode, steps, warmup,
+                                       ceiling))
     return out
 
 
@@ -151,6 +153,12 @@ def main(argv=None) -> int:
     ap.add_argument("--modes", default="streaming,hot")
     ap.add_argument("--variant", action="append", default=[], metavar="OP=V1,V2",
                     help="variants to time for an op (default: its incumbent)")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the read ceiling (profiling runs)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB, the "
+                         "known-size reference of counter (FETCH_SIZE / "
+                         "WRITE_SIZE) runs")
     a = ap.parse_args(argv)
     ops = tuple(o for o in a.ops.split(",") if o)
     if not ops or any(o not in OPS for o in ops):
@@ -174,8 +182,15 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("sweep: no GPU visible", file=sys.stderr)
         return 1
+    if a.calib_copy_mib:
+        src = torch.empty(a.calib_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     recs = run(ops=ops, shapes=shapes, modes=modes, steps=a.steps, warmup=a.warmup,
-               variants=variants)
+               variants=variants, ceiling=not a.no_ceiling)
     print(table(recs), flush=True)
     print("\n" + speedups(recs), flush=True)
     if a.json:
