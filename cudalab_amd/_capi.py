@@ -15,7 +15,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-from .build import LIB_PATH, source_hash
+from .build import FAST_NAME, LIB_PATH, fast_module_path, source_hash
 
 CQ_OK = 0
 CQ_ERR_UNKNOWN_VARIANT = 1
@@ -73,6 +73,11 @@ class CqProblem(ctypes.Structure):
     ]
 
 
+class CqPrepared(ctypes.Structure):
+    """cq_prepared_t: a launch resolved by cq_prepare (opaque)."""
+    _fields_ = [("opaque", ctypes.c_uint64 * 12)]
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _cstr = ctypes.c_char_p
@@ -115,6 +120,9 @@ SIGNATURES = {
     "cq_describe_launch": (ctypes.c_int, [ctypes.c_int, _cstr, _i64, _i64,
                                           _vp, _vp, ctypes.c_char_p,
                                           ctypes.c_size_t]),
+    "cq_prepare": (ctypes.c_int, [ctypes.c_int, _cstr, _vp, _vp, _vp, _vp,
+                                  _i64, _i64, ctypes.POINTER(CqPrepared)]),
+    "cq_launch_prepared": (ctypes.c_int, [_vp, _vp]),
     "cq_last_error": (ctypes.c_char_p, []),
     "cq_version": (ctypes.c_char_p, []),
 }
@@ -163,6 +171,44 @@ def load():
                 "`python -m cudalab_amd.build` (or __graft_entry__.build()).")
         _lib = lib
         return lib
+
+
+_fast = None
+
+
+def fast_module():
+    """The eager fast-path module (`_cqfast`, built beside the library from
+    csrc/cq_pyfast.cpp), loaded once; refused, like the library, when
+    missing or built from other sources than the tree holds."""
+    global _fast
+    if _fast is not None:
+        return _fast
+    load()
+    with _lock:
+        if _fast is not None:
+            return _fast
+        import importlib.util
+        path = fast_module_path()
+        if not path.exists():
+            raise LibraryMissing(
+                f"{path} is not built; run `python -m cudalab_amd.build` "
+                "(or __graft_entry__.build()).")
+        spec = importlib.util.spec_from_file_location(FAST_NAME, path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        if mod.src_hash != source_hash():
+            raise StaleLibrary(
+                f"{path} was built from other sources than the tree holds "
+                f"(module src={mod.src_hash}, tree src={source_hash()}); rebuild "
+                "it with `python -m cudalab_amd.build`.")
+        _fast = mod
+        return mod
+
+
+def entry_address(name: str) -> int:
+    """Address of a library entry point (for the fast-path module, which
+    calls the same loaded library)."""
+    return ctypes.cast(getattr(load(), name), ctypes.c_void_p).value
 
 
 def library_stamp(lib) -> str:

@@ -46,6 +46,10 @@ LIB_PATH = LIB_DIR / LIB_NAME
 
 ARCH = "gfx950"
 SOURCES = ("cq_kernels.hip", "cq_quantize.hip", "cq_capi.cpp")
+# the Python binding of the eager fast path (host code only, built with the
+# host compiler against torch's headers; it calls the library by address)
+FAST_SOURCE = "cq_pyfast.cpp"
+FAST_NAME = "_cqfast"
 HIPCC_FLAGS = (
     f"--offload-arch={ARCH}",
     "-O3",
@@ -100,8 +104,33 @@ def _run(cmd: list[str]) -> None:
         print(log, file=sys.stderr)
 
 
+def fast_module_path() -> Path:
+    import sysconfig
+    return LIB_DIR / (FAST_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _fast_module_cmd(out: Path, stamp: str) -> list[str]:
+    """g++ line of the fast-path module: torch's and Python's headers, HIP's
+    host headers (for the current-stream query), linked against torch's
+    libraries, which the importing process has already loaded."""
+    import sysconfig
+
+    import torch
+    from torch.utils.cpp_extension import include_paths, library_paths
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    incs = [*include_paths(), sysconfig.get_paths()["include"],
+            str(Path(rocm) / "include"), str(INCLUDE)]
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+            f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+            stamp, *[f"-I{p}" for p in incs], str(CSRC / FAST_SOURCE),
+            "-o", str(out), *[f"-L{p}" for p in library_paths()],
+            "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+
+
 def build_library(verbose: bool = False) -> Path:
-    """Compile `libcdnaqgemv.so` in-tree (always compiles; atomic replace)."""
+    """Compile `libcdnaqgemv.so` and the fast-path module in-tree (always
+    compiles; atomic replace)."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="cq_build_", dir=LIB_DIR) as tmp:
@@ -113,9 +142,12 @@ def build_library(verbose: bool = False) -> Path:
             objs.append(str(obj))
             cmds.append([cc, *HIPCC_FLAGS, stamp, f"-I{INCLUDE}", f"-I{CSRC}",
                          "-c", str(CSRC / src), "-o", str(obj)])
+        fast_tmp = Path(tmp) / fast_module_path().name
+        cmds.append(_fast_module_cmd(fast_tmp, stamp))
         with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
             for f in [ex.submit(_run, c) for c in cmds]:
                 f.result()
+        os.replace(fast_tmp, fast_module_path())
         out_tmp = Path(tmp) / LIB_NAME
         _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs,
               "-o", str(out_tmp)])

@@ -24,6 +24,7 @@
 #include <cstring>
 #include <numeric>
 #include <string>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -233,6 +234,33 @@ hipError_t launch_plan(int op, const cq::Plan& p, const void* w,
     if (op == CQ_OP_QGEMV)
         return cq::launch_q8(p, w, scale, x, y, n, k, stream, ev0, ev1);
     return cq::launch_gemv(p, gemv_dtype(op), w, x, y, n, k, stream, ev0, ev1);
+}
+
+hipError_t prepare_plan(int op, const cq::Plan& p, const void* w,
+                        const void* scale, const void* x, void* y, int64_t n,
+                        int64_t k, cq::Launch* out) {
+    if (op == CQ_OP_INT4GEMV) return cq::prepare_int4(p, w, scale, x, y, n, k, out);
+    if (op == CQ_OP_QGEMV) return cq::prepare_q8(p, w, scale, x, y, n, k, out);
+    return cq::prepare_gemv(p, gemv_dtype(op), w, x, y, n, k, out);
+}
+
+// Layout of a filled cq_prepared_t: a magic word, a seal over the launch
+// record (FNV-1a of its bytes, keyed by the magic) and the record itself.
+struct Prepared {
+    uint64_t magic;
+    uint64_t seal;
+    cq::Launch launch;
+};
+static_assert(sizeof(Prepared) <= sizeof(cq_prepared_t), "cq_prepared_t too small");
+static_assert(std::is_trivially_copyable_v<cq::Launch>);
+constexpr uint64_t kPreparedMagic = 0x31766d6771616463ull;  // "cdaqgmv1"
+
+uint64_t seal_of(const cq::Launch& L) {
+    unsigned char bytes[sizeof(cq::Launch)];
+    std::memcpy(bytes, &L, sizeof bytes);
+    uint64_t h = 0xcbf29ce484222325ull ^ kPreparedMagic;
+    for (unsigned char b : bytes) h = (h ^ b) * 0x100000001b3ull;
+    return h;
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -720,6 +748,37 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
                   p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
                   p.why.empty() ? "-" : p.why.c_str());
     return write_out(line, buf, cap);
+}
+
+int cq_prepare(int op, const char* variant, const void* w, const void* scale,
+               const void* x, void* y, int64_t n, int64_t k, cq_prepared_t* out) {
+    g_last_error.clear();
+    if (out == nullptr) return fail(CQ_ERR_INVALID_ARG, "prepared record pointer is NULL");
+    std::memset(out, 0, sizeof *out);
+    if (is_gemv(op)) scale = nullptr;
+    const Variant* v = nullptr;
+    const int st = check_launch(op, variant, &v, w, scale, x, y, n, k);
+    if (st != CQ_OK) return st;
+    const cq::Plan p = make_plan(op, *v, n, k, w, x);
+    Prepared rec{};
+    const hipError_t e = prepare_plan(op, p, w, scale, x, y, n, k, &rec.launch);
+    if (e != hipSuccess) return hip_fail(e, "launch preparation");
+    rec.magic = kPreparedMagic;
+    rec.seal = seal_of(rec.launch);
+    std::memcpy(out, &rec, sizeof rec);
+    return CQ_OK;
+}
+
+int cq_launch_prepared(const cq_prepared_t* prepared, void* stream) {
+    if (prepared == nullptr) return fail(CQ_ERR_INVALID_ARG, "prepared record pointer is NULL");
+    Prepared rec;
+    std::memcpy(&rec, prepared, sizeof rec);
+    if (rec.magic != kPreparedMagic || rec.seal != seal_of(rec.launch))
+        return fail(CQ_ERR_INVALID_ARG, "not a record filled by cq_prepare (or damaged)");
+    const hipError_t e = cq::enqueue(rec.launch, static_cast<hipStream_t>(stream),
+                                     nullptr, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return CQ_OK;
 }
 
 const char* cq_last_error(void) { return g_last_error.c_str(); }

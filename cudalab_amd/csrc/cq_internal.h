@@ -46,6 +46,28 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
 bool int4_contract_ok(const void* w, const void* x, int64_t k);
 bool q8_contract_ok(const void* w, const void* x, int64_t k);
 
+// A launch resolved to its kernel instance, shape and arguments: plain data
+// holding no pointer into the library's state (the kernel address is the
+// instance's host-side handle), built once and enqueued any number of times,
+// on any stream of the device whose operands it names.  Each kernel argument
+// sits in its own 8-byte slot.
+constexpr int kMaxLaunchArgs = 6;
+struct Launch {
+    const void* fn = nullptr;
+    uint32_t grid = 0, block = 0, shmem = 0, nargs = 0;
+    uint64_t args[kMaxLaunchArgs] = {};
+};
+
+// Resolve `plan` on the given operands into a Launch (no GPU call).
+hipError_t prepare_int4(const Plan& plan, const void* w, const void* scale,
+                        const void* x, void* y, int64_t n, int64_t k, Launch* out);
+hipError_t prepare_q8(const Plan& plan, const void* w, const void* scale,
+                      const void* x, void* y, int64_t n, int64_t k, Launch* out);
+
+// Enqueue a resolved launch on `stream`; ev0/ev1 as below.
+hipError_t enqueue(const Launch& launch, hipStream_t stream, hipEvent_t ev0,
+                   hipEvent_t ev1);
+
 // Enqueue one launch of `plan` on `stream`.  ev0/ev1, when non-null, are
 // attached to the dispatch itself (start/stop of the kernel).
 hipError_t launch_int4(const Plan& plan, const void* w, const void* scale,
@@ -83,6 +105,8 @@ enum Dtype : int { kF16 = 0, kF32 = 1 };
 bool gemv_contract_ok(int dtype, const void* w, const void* x, int64_t k);
 Plan plan_gemv(int kind, int dtype, int64_t n, int64_t k, const void* w,
                const void* x);
+hipError_t prepare_gemv(const Plan& plan, int dtype, const void* w,
+                        const void* x, void* y, int64_t n, int64_t k, Launch* out);
 hipError_t launch_gemv(const Plan& plan, int dtype, const void* w,
                        const void* x, void* y, int64_t n, int64_t k,
                        hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);

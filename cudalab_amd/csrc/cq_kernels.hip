@@ -50,6 +50,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstring>
 #include <type_traits>
 
 namespace cq {
@@ -1290,6 +1291,28 @@ hipError_t launch(void (*kernel)(Params...), int64_t grid, int block,
                               argv, shmem, stream, ev0, ev1, 0);
 }
 
+// The same launch resolved into a Launch record instead of enqueued: the
+// kernel, its shape and its arguments, each argument copied into an 8-byte
+// slot (the runtime reads each argument's own size from the slot's start).
+template <typename... Params>
+hipError_t bind(Launch* out, void (*kernel)(Params...), int64_t grid,
+                int block, uint32_t shmem, std::type_identity_t<Params>... args) {
+    static_assert(sizeof...(Params) <= kMaxLaunchArgs, "too many kernel arguments");
+    static_assert(((sizeof(Params) <= 8 && std::is_trivially_copyable_v<Params>) && ...),
+                  "kernel arguments must fit an 8-byte slot");
+    if (grid < 1 || grid > UINT32_MAX) return hipErrorInvalidConfiguration;
+    Launch L;
+    L.fn = reinterpret_cast<const void*>(kernel);
+    L.grid = static_cast<uint32_t>(grid);
+    L.block = static_cast<uint32_t>(block);
+    L.shmem = shmem;
+    L.nargs = sizeof...(Params);
+    int i = 0;
+    ((std::memcpy(&L.args[i++], &args, sizeof(args))), ...);
+    *out = L;
+    return hipSuccess;
+}
+
 int pow2_at_least(int64_t v, int lo) {
     int p = lo;
     while (p < v && p < 64) p <<= 1;
@@ -1448,15 +1471,13 @@ Plan plan_q8(int kind, int rows, int64_t n, int64_t k, const void* w,
     return p;
 }
 
-hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
-                       const void* x, void* y, int64_t n, int64_t k,
-                       hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+hipError_t prepare_int4(const Plan& p, const void* w, const void* scale,
+                        const void* x, void* y, int64_t n, int64_t k, Launch* L) {
     if (p.kind == kScalar)
-        return launch(int4gemv_scalar_kernel, p.grid, p.block, 0, stream, ev0,
-                      ev1, static_cast<const uint8_t*>(w),
-                      static_cast<const uint16_t*>(scale),
-                      static_cast<const uint16_t*>(x),
-                      static_cast<uint16_t*>(y), k);
+        return bind(L, int4gemv_scalar_kernel, p.grid, p.block, 0,
+                    static_cast<const uint8_t*>(w),
+                    static_cast<const uint16_t*>(scale),
+                    static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), k);
     if (p.kind == kTiled) {
         const Int4Fn tfn =
             p.r == 1 && p.tile == 7   ? &int4gemv_tiled_kernel<kBlock, 7, 1>
@@ -1464,11 +1485,10 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
             : p.r == 2 && p.tile == 4 ? &int4gemv_tiled_kernel<kBlock, 4, 2>
                                       : nullptr;
         if (tfn == nullptr) return hipErrorInvalidConfiguration;
-        return launch(tfn, p.grid, kBlock, tile_lds(4, p.tile), stream, ev0, ev1,
-                      static_cast<const uint4*>(w),
-                      static_cast<const uint16_t*>(scale),
-                      static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
-                      static_cast<int>(n), static_cast<int>(k / 32));
+        return bind(L, tfn, p.grid, kBlock, tile_lds(4, p.tile),
+                    static_cast<const uint4*>(w), static_cast<const uint16_t*>(scale),
+                    static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
+                    static_cast<int>(n), static_cast<int>(k / 32));
     }
     const Int4Fn fn =
         p.kind == kWave ? instance<Int4Wave>(p.cw, p.j, p.r)
@@ -1477,31 +1497,27 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     if (p.kind == kLds && !lds_chunks_ok(p, k / 32)) return hipErrorInvalidConfiguration;
     const uint32_t shmem = p.kind == kLds ? int4_lds_bytes(p.cw, p.j) : 0;
-    return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
-                  static_cast<const uint4*>(w),
-                  static_cast<const uint16_t*>(scale),
-                  static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
-                  static_cast<int>(n), static_cast<int>(k / 32));
+    return bind(L, fn, p.grid, p.block, shmem, static_cast<const uint4*>(w),
+                static_cast<const uint16_t*>(scale), static_cast<const uint4*>(x),
+                static_cast<uint16_t*>(y), static_cast<int>(n),
+                static_cast<int>(k / 32));
 }
 
-hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
-                     const void* x, void* y, int64_t n, int64_t k,
-                     hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+hipError_t prepare_q8(const Plan& p, const void* w, const void* scale,
+                      const void* x, void* y, int64_t n, int64_t k, Launch* L) {
     if (p.kind == kScalar)
-        return launch(qgemv_scalar_kernel, p.grid, p.block, 0, stream, ev0,
-                      ev1, static_cast<const int8_t*>(w),
-                      static_cast<const float*>(scale),
-                      static_cast<const uint16_t*>(x),
-                      static_cast<uint16_t*>(y), k);
+        return bind(L, qgemv_scalar_kernel, p.grid, p.block, 0,
+                    static_cast<const int8_t*>(w), static_cast<const float*>(scale),
+                    static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), k);
     if (p.kind == kTiled) {
         const Q8Fn tfn = p.r == 2 && p.tile == q8_tile_j(2) ? &qgemv_tiled_kernel<kBlock, q8_tile_j(2), 2>
                          : p.r == 1 && p.tile == q8_tile_j(1) ? &qgemv_tiled_kernel<kBlock, q8_tile_j(1), 1>
                                                                : nullptr;
         if (tfn == nullptr) return hipErrorInvalidConfiguration;
-        return launch(tfn, p.grid, kBlock, tile_lds(2, p.tile), stream, ev0, ev1,
-                      static_cast<const uint4*>(w), static_cast<const float*>(scale),
-                      static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
-                      static_cast<int>(n), static_cast<int>(k / 16));
+        return bind(L, tfn, p.grid, kBlock, tile_lds(2, p.tile),
+                    static_cast<const uint4*>(w), static_cast<const float*>(scale),
+                    static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
+                    static_cast<int>(n), static_cast<int>(k / 16));
     }
     const Q8Fn fn = p.kind == kWave ? instance<Q8Wave>(p.cw, p.j, p.r)
                     : p.block == 512 ? instance<Q8Lds<512>>(p.cw, p.j, p.r)
@@ -1509,10 +1525,38 @@ hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
     if (fn == nullptr) return hipErrorInvalidConfiguration;
     if (p.kind == kLds && !lds_chunks_ok(p, k / 16)) return hipErrorInvalidConfiguration;
     const uint32_t shmem = p.kind == kLds ? q8_lds_bytes(p.cw, p.j) : 0;
-    return launch(fn, p.grid, p.block, shmem, stream, ev0, ev1,
-                  static_cast<const uint4*>(w), static_cast<const float*>(scale),
-                  static_cast<const uint4*>(x), static_cast<uint16_t*>(y),
-                  static_cast<int>(n), static_cast<int>(k / 16));
+    return bind(L, fn, p.grid, p.block, shmem, static_cast<const uint4*>(w),
+                static_cast<const float*>(scale), static_cast<const uint4*>(x),
+                static_cast<uint16_t*>(y), static_cast<int>(n),
+                static_cast<int>(k / 16));
+}
+
+hipError_t enqueue(const Launch& L, hipStream_t stream, hipEvent_t ev0,
+                   hipEvent_t ev1) {
+    if (L.fn == nullptr || L.nargs > kMaxLaunchArgs) return hipErrorInvalidConfiguration;
+    void* argv[kMaxLaunchArgs];
+    for (uint32_t i = 0; i < L.nargs; ++i)
+        argv[i] = const_cast<uint64_t*>(&L.args[i]);
+    const dim3 g(L.grid), b(L.block);
+    if (ev0 == nullptr && ev1 == nullptr)
+        return hipLaunchKernel(L.fn, g, b, argv, L.shmem, stream);
+    return hipExtLaunchKernel(L.fn, g, b, argv, L.shmem, stream, ev0, ev1, 0);
+}
+
+hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
+                       const void* x, void* y, int64_t n, int64_t k,
+                       hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    Launch L;
+    const hipError_t e = prepare_int4(p, w, scale, x, y, n, k, &L);
+    return e != hipSuccess ? e : enqueue(L, stream, ev0, ev1);
+}
+
+hipError_t launch_q8(const Plan& p, const void* w, const void* scale,
+                     const void* x, void* y, int64_t n, int64_t k,
+                     hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    Launch L;
+    const hipError_t e = prepare_q8(p, w, scale, x, y, n, k, &L);
+    return e != hipSuccess ? e : enqueue(L, stream, ev0, ev1);
 }
 
 namespace {
@@ -1711,34 +1755,38 @@ GemvFn<S> gemv_instance(int cw, int j, int block) {
 }
 
 template <typename S>
-hipError_t launch_gemv_t(const Plan& p, const void* w, const void* x, void* y,
-                         int64_t n, int64_t k, hipStream_t stream,
-                         hipEvent_t ev0, hipEvent_t ev1) {
+hipError_t prepare_gemv_t(const Plan& p, const void* w, const void* x, void* y,
+                          int64_t n, int64_t k, Launch* L) {
     if (p.kind == kScalar)
-        return launch(gemv_scalar_kernel<S>, p.grid, p.block, 0, stream, ev0,
-                      ev1, static_cast<const S*>(w), static_cast<const S*>(x),
-                      static_cast<S*>(y), k);
+        return bind(L, gemv_scalar_kernel<S>, p.grid, p.block, 0,
+                    static_cast<const S*>(w), static_cast<const S*>(x),
+                    static_cast<S*>(y), k);
     const int nchunks = static_cast<int>(k * static_cast<int64_t>(sizeof(S)) / 16);
     if (p.kind == kTiled)
-        return launch(p.block == 512 ? gemv_tiled_kernel<S, 512> : gemv_tiled_kernel<S, kBlock>,
-                      p.grid, p.block, kGemvTileLds, stream, ev0, ev1,
-                      static_cast<const uint4*>(w), static_cast<const uint4*>(x),
-                      static_cast<S*>(y), static_cast<int>(n), nchunks);
+        return bind(L, p.block == 512 ? gemv_tiled_kernel<S, 512> : gemv_tiled_kernel<S, kBlock>,
+                    p.grid, p.block, kGemvTileLds, static_cast<const uint4*>(w),
+                    static_cast<const uint4*>(x), static_cast<S*>(y),
+                    static_cast<int>(n), nchunks);
     const GemvFn<S> fn = gemv_instance<S>(p.cw, p.j, p.block);
     if (fn == nullptr) return hipErrorInvalidConfiguration;
-    return launch(fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),
-                  stream, ev0, ev1, static_cast<const uint4*>(w),
-                  static_cast<const uint4*>(x), static_cast<S*>(y),
-                  static_cast<int>(n), nchunks);
+    return bind(L, fn, p.grid, p.block, static_cast<uint32_t>((nchunks + 1) * 16),
+                static_cast<const uint4*>(w), static_cast<const uint4*>(x),
+                static_cast<S*>(y), static_cast<int>(n), nchunks);
 }
 }  // namespace
+
+hipError_t prepare_gemv(const Plan& p, int dtype, const void* w, const void* x,
+                        void* y, int64_t n, int64_t k, Launch* L) {
+    return dtype == kF32 ? prepare_gemv_t<float>(p, w, x, y, n, k, L)
+                         : prepare_gemv_t<uint16_t>(p, w, x, y, n, k, L);
+}
 
 hipError_t launch_gemv(const Plan& p, int dtype, const void* w, const void* x,
                        void* y, int64_t n, int64_t k, hipStream_t stream,
                        hipEvent_t ev0, hipEvent_t ev1) {
-    return dtype == kF32
-               ? launch_gemv_t<float>(p, w, x, y, n, k, stream, ev0, ev1)
-               : launch_gemv_t<uint16_t>(p, w, x, y, n, k, stream, ev0, ev1);
+    Launch L;
+    const hipError_t e = prepare_gemv(p, dtype, w, x, y, n, k, &L);
+    return e != hipSuccess ? e : enqueue(L, stream, ev0, ev1);
 }
 
 hipError_t launch_stream_read(const void* buf, int64_t bytes, void* sink,

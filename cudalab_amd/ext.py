@@ -9,10 +9,20 @@ validation order, and the same message substrings, which callers match
 Every check runs on host metadata before anything is launched and raises
 RuntimeError (the type TORCH_CHECK surfaced as).
 
-What differs by design: validation lives here, in Python, where the CPU
-test suite can reach it; the C layer receives plain pointers and sizes and
-picks the kernel (vectorized or scalar fallback) from alignment.  Launches
-go on the current torch stream of the weights' device.
+What differs by design: the checks that raise live here, in Python, where
+the CPU test suite can reach them; the C layer receives plain pointers and
+sizes and picks the kernel (vectorized or scalar fallback) from alignment.
+Launches go on the current torch stream of the weights' device.
+
+`forward` and `forward_into` first offer the call to the fast path
+(csrc/cq_pyfast.cpp): one C++ call that applies the same acceptance rule to
+the tensors' metadata, looks the launch up in a cache of launches prepared
+once by cq_prepare (keyed by variant, operand addresses and sizes, so a
+cached launch is exactly what preparing again would give) and enqueues it.
+It launches nothing for a call it does not accept, and the checked path
+below then runs and raises in the reference's order.  On MI355X this took
+an INT4 forward_into from 8.2 us of host time to about 3 us, of which
+hipLaunchKernel itself is 2.2 us.
 """
 from __future__ import annotations
 
@@ -43,6 +53,18 @@ NATIVE_TIMING_NOTE = (
     "the profiler's per-dispatch kernel duration)")
 
 
+# prepared launches kept per operator (the cache is cleared when full)
+FAST_CACHE_ENTRIES = 4096
+_FAST_KIND = {"int4gemv": 0, "qgemv": 1, "gemv": 2}
+
+
+def _fast_launcher(op: str, names: list[str]):
+    return _capi.fast_module().Launcher(
+        _FAST_KIND[op], names, _capi.entry_address("cq_prepare"),
+        _capi.entry_address("cq_launch_prepared"),
+        _capi.entry_address("cq_last_error"), FAST_CACHE_ENTRIES)
+
+
 def _fail(msg: str) -> None:
     raise RuntimeError(msg)
 
@@ -67,6 +89,7 @@ class _OpExt:
         self._grouped_fn = (self._lib.cq_int4gemv_grouped
                             if self.op == "int4gemv"
                             else self._lib.cq_qgemv_grouped)
+        self._fast = _fast_launcher(self.op, self._all + sorted(self._aliases))
 
     # ---- registry (bindings.cpp variant lists) ----
     def variants(self) -> list[str]:
@@ -152,6 +175,9 @@ class _OpExt:
     def forward(self, variant: str, W: torch.Tensor, scale: torch.Tensor,
                 x: torch.Tensor) -> torch.Tensor:
         """y = W_dequant @ x into a newly allocated fp16 (N,) tensor."""
+        y = self._fast.forward(variant, W, scale, x)
+        if y is not None:
+            return y
         self._lookup(variant)
         self._validate_inputs(W, scale, x)
         out = torch.empty(W.size(0), dtype=torch.float16, device=W.device)
@@ -162,6 +188,8 @@ class _OpExt:
                      scale: torch.Tensor, x: torch.Tensor,
                      out: torch.Tensor) -> None:
         """Same as forward, writing into a preallocated `out` (N,) fp16."""
+        if self._fast.into(variant, W, scale, x, out):
+            return
         self._lookup(variant)
         self._validate_inputs(W, scale, x)
         self._validate_out(W, out)
@@ -481,6 +509,9 @@ class GemvExt(_OpExt):
     def forward(self, variant: str, W: torch.Tensor,  # type: ignore[override]
                 x: torch.Tensor) -> torch.Tensor:
         """y = W @ x (FP32 accumulation) into a new (N,) tensor of W's dtype."""
+        y = self._fast.gemv_forward(variant, W, x)
+        if y is not None:
+            return y
         self._lookup(variant)
         self._validate_w(W)
         self._validate_x(W, x)
@@ -490,6 +521,8 @@ class GemvExt(_OpExt):
 
     def forward_into(self, variant: str, W: torch.Tensor,  # type: ignore[override]
                      x: torch.Tensor, out: torch.Tensor) -> None:
+        if self._fast.gemv_into(variant, W, x, out):
+            return
         self._lookup(variant)
         self._validate_w(W)
         self._validate_x(W, x)

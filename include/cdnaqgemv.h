@@ -316,6 +316,43 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
                        const void* w, const void* x, char* buf, size_t cap);
 
 /*
+ * A launch resolved ahead of time: opaque plain data, no resources held.
+ * Zero-initialised or damaged records are refused by cq_launch_prepared.
+ */
+typedef struct cq_prepared {
+    uint64_t opaque[12];
+} cq_prepared_t;
+
+/*
+ * Runs every check and the plan of one cq_int4gemv (op = CQ_OP_INT4GEMV),
+ * cq_qgemv (CQ_OP_QGEMV) or cq_gemv (CQ_OP_GEMV_F16 / CQ_OP_GEMV_F32;
+ * `scale` ignored) call, with the same arguments and the same status and
+ * cq_last_error() on failure, and stores the resolved launch (kernel
+ * instance, grid, block, LDS bytes, arguments) in *out instead of
+ * enqueueing it.  On failure *out is zeroed.  Nothing is launched and no
+ * GPU call is made.
+ *
+ * No counterpart in the reference: its pybind modules validate and launch
+ * in one call (kernels/int4gemv/bindings.cpp:145-176,
+ * kernels/qgemv/bindings.cpp:140-173).  For callers that issue the same
+ * GEMV on the same buffers many times from the host (a decode loop, an
+ * eager Python API that caches per operand set), so that the checks are
+ * paid once.
+ */
+int cq_prepare(int op, const char* variant, const void* w, const void* scale,
+               const void* x, void* y, int64_t n, int64_t k, cq_prepared_t* out);
+
+/*
+ * Enqueues a prepared launch on `stream` (NULL = the default stream).  The
+ * stream must belong to the device that was current at cq_prepare, and the
+ * buffers named there must still be allocated: the record holds raw device
+ * pointers and is not re-validated beyond its integrity check
+ * (CQ_ERR_INVALID_ARG for a record cq_prepare did not fill).  Results are
+ * bit-identical to the direct call.  Returns CQ_OK or CQ_ERR_HIP.
+ */
+int cq_launch_prepared(const cq_prepared_t* prepared, void* stream);
+
+/*
  * Message of the last failed call on this thread ("" if none).  Replaces
  * the TORCH_CHECK error text that the reference's pybind layer raised.
  */
