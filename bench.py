@@ -63,6 +63,9 @@ ROOT = Path(__file__).resolve().parent
 BASELINE = json.loads((ROOT / "BASELINE.json").read_text())
 METRIC = BASELINE["metric"]
 HBM_PEAK_GBS = 8000.0
+# launches per window of the secondary figures in `detail` (INT4 windows,
+# hot, INT8, read ceiling, launch floor), at least --steps
+DETAIL_LAUNCHES = 2000
 TRAFFIC_FILE = ROOT / "profiles" / "int4gemv_4096x4096_streaming_traffic.json"
 
 
@@ -457,13 +460,15 @@ def main(argv=None) -> int:
     ceil = floor_us = None
     if not args.no_detail:
         from cudalab_amd.ext import launch_floor, prefill_delay_us, read_ceiling
-        nl = max(args.steps, 200)
+        # every secondary window has one fixed length whatever --steps says,
+        # so INT4, INT8, hot, the ceiling and the floor compare like for like
+        nl = max(args.steps, DETAIL_LAUNCHES)
         ceil = read_ceiling(nbytes, warmup=args.warmup, n_launches=nl,
                             burn_ms=100.0, delay_us=prefill_delay_us(nl))
         floor_us = launch_floor(int(plan["grid"]), int(plan["block"]),
                                 warmup=args.warmup, n_launches=nl, burn_ms=100.0,
                                 delay_us=prefill_delay_us(nl))
-        w4 = windows("int4gemv", args.variant, sets, args.steps)
+        w4 = windows("int4gemv", args.variant, sets, nl)
         detail["int4_5_windows_us"] = {k: round(v, 4) for k, v in w4.items()}
         detail["graph_us_per_call"] = round(graph_loop(ext4, args.variant, sets), 4)
         if args.mode == "streaming" and len(sets) >= 16:
@@ -474,19 +479,19 @@ def main(argv=None) -> int:
                                        "(cq_int4gemv_grouped) over distinct HBM-cold "
                                        "sets, from a HIP graph: the per-launch cost "
                                        "shared by 8 GEMVs; not the headline caliber")
-        gpu_loop("int4gemv", args.variant, sets[:1], args.steps, args.warmup, 100.0)
-        h = windows("int4gemv", args.variant, sets[:1], args.steps)
+        gpu_loop("int4gemv", args.variant, sets[:1], nl, args.warmup, 100.0)
+        h = windows("int4gemv", args.variant, sets[:1], nl)
         detail["hot_us_per_call"] = round(h["median"], 4)
         detail["hot_GBps"] = round(nbytes / h["median"] / 1e3, 1)
         build("qgemv")
         q_sets, q_bytes = make_sets("qgemv", N, K, args.mode)
-        gpu_loop("qgemv", "qgemv_cdna4", q_sets, args.steps, args.warmup, 100.0)
-        q = windows("qgemv", "qgemv_cdna4", q_sets, args.steps)
+        gpu_loop("qgemv", "qgemv_cdna4", q_sets, nl, args.warmup, 100.0)
+        q = windows("qgemv", "qgemv_cdna4", q_sets, nl)
         detail["int8_us_per_call"] = round(q["median"], 4)
         detail["int8_GBps"] = round(q_bytes / q["median"] / 1e3, 1)
         detail["speedup_int4_vs_int8"] = round(q["median"] / w4["median"], 3)
         detail["speedup_note"] = ("INT8 and INT4 medians of 5 pre-filled windows of "
-                                  f"{args.steps} launches each, streaming, same shape")
+                                  f"{nl} launches each, streaming, same shape")
         del q_sets
         torch.cuda.empty_cache()
     cpu = None

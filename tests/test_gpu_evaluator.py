@@ -87,3 +87,16 @@ def test_launch_floor_and_read_ceiling(ext4):
     for grid, block in ((0, 256), (256, 0), (256, 1025)):
         with pytest.raises(RuntimeError, match="grid must be"):
             E.launch_floor(grid, block, warmup=0, n_launches=1)
+
+
+def test_api_cost_paths_all_launch(cuda):
+    """The host-cost tool times real launches on every path: each raw entry
+    point is status-checked before and after, and no path can read below
+    the cost of an enqueue (a refused call returns in ~0.1 us)."""
+    from cudalab_amd.evaluator import api_cost
+    res = api_cost.run(n=1024, k=1024, calls=50, reps=2)
+    floor = res["native_enqueue_us_per_launch"]
+    assert floor > 0.5
+    for name, rec in res["host_us_per_call"].items():
+        assert rec["us"] is not None and rec["samples"] == 2, name
+        assert rec["us"] > 0.5 * floor, (name, rec, floor)
