@@ -21,8 +21,8 @@ once by cq_prepare (keyed by variant, operand addresses and sizes, so a
 cached launch is exactly what preparing again would give) and enqueues it.
 It launches nothing for a call it does not accept, and the checked path
 below then runs and raises in the reference's order.  On MI355X this took
-an INT4 forward_into from 8.2 us of host time to about 3 us, of which
-hipLaunchKernel itself is 2.2 us.
+an INT4 forward_into from 7.0-8.2 us of host time to 3.0-3.2 us, within
+0.1-0.7 us of hipLaunchKernel itself (2.2-3.1 us depending on the host).
 """
 from __future__ import annotations
 
