@@ -31,6 +31,12 @@ All three produce bit-identical outputs.
 Usage: python -m cudalab_amd.decode [--model 7b|70b] [--layers N]
        [--op int4gemv|qgemv] [--steps 20] [--warmup 3]
        [--modes sequential,grouped,graph]
+       python -m cudalab_amd.decode --stress [--op int4gemv|qgemv] [--steps 20]
+
+--stress times the decode stress sequence of the measurement plan instead:
+(N, K) = (11008, 4096), (4096, 11008), then four (4096, 4096), back to back,
+over an HBM-cold pool of distinct weights, replayed from a HIP graph and
+run eager.
 """
 from __future__ import annotations
 
@@ -199,6 +205,56 @@ def time_steps(fn, steps: int, warmup: int) -> float:
 
 MODES = ("sequential", "grouped", "graph")
 
+# The decode stress sequence of the measurement plan: the 7B MLP pair, then
+# four 4096^2 projections, back to back (each launch's input is its own x).
+STRESS_SHAPES = ((11008, 4096), (4096, 11008), (4096, 4096), (4096, 4096),
+                 (4096, 4096), (4096, 4096))
+STRESS_POOL_BYTES = 512 << 20
+
+
+def stress(op: str = "int4gemv", replays: int = 20, warmup: int = 3,
+           pool_bytes: int = STRESS_POOL_BYTES) -> dict:
+    """The stress sequence over HBM-cold weights: enough distinct copies of
+    the six (W, scale, x, out) sets that together they exceed `pool_bytes`
+    (twice the 256 MB MALL by default), all sequences launched back to back
+    through forward_into, captured once in a HIP graph and replayed.  Also
+    the same launches eager (the Python API path of every call).  Returns
+    µs per sequence and per GEMV and the effective weight bandwidth."""
+    from .operators import int4gemv as op4
+    from .operators import qgemv as op8
+    mod, nbytes_of = ((op4, op4.int4_bytes) if op == "int4gemv"
+                      else (op8, op8.q8_bytes))
+    seq_bytes = sum(nbytes_of(N, K) for N, K in STRESS_SHAPES)
+    nseq = max(2, -(-pool_bytes // seq_bytes))
+    ext, variant = build(op), VARIANT[op]
+    seqs = [[mod.device_random_set(N, K, 7919 * i + j)
+             for j, (N, K) in enumerate(STRESS_SHAPES)] for i in range(nseq)]
+
+    def all_sequences():
+        for seq in seqs:
+            for W, sc, x, out in seq:
+                ext.forward_into(variant, W, sc, x, out)
+
+    all_sequences()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=side):
+        all_sequences()
+    torch.cuda.synchronize()
+    res = {"op": op, "variant": variant, "shapes": [list(s) for s in STRESS_SHAPES],
+           "sequences_in_pool": nseq, "pool_bytes": nseq * seq_bytes,
+           "bytes_per_sequence": seq_bytes,
+           "note": "one replay runs every sequence of the pool once; each sequence "
+                   "is six dependent-free launches on one stream"}
+    for mode, fn in (("graph", g.replay), ("eager", all_sequences)):
+        us = time_steps(fn, replays, warmup) / nseq
+        res[mode] = {"us_per_sequence": round(us, 2),
+                     "us_per_gemv": round(us / len(STRESS_SHAPES), 3),
+                     "GBps": round(seq_bytes / us / 1e3, 1),
+                     "frac_peak": round(seq_bytes / us / 1e3 / 8000.0, 4)}
+    return res
+
 
 def run(op: str = "int4gemv", layers: int | None = None, steps: int = 20,
         warmup: int = 3, modes=MODES, model: str = "7b") -> dict:
@@ -238,7 +294,16 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--modes", default=",".join(MODES),
                     help="comma-separated subset of " + ",".join(MODES))
+    ap.add_argument("--stress", action="store_true",
+                    help="time the decode stress sequence (11008x4096, 4096x11008, "
+                         "4 x 4096x4096) over an HBM-cold pool instead of a model")
     a = ap.parse_args(argv)
+    if a.stress:
+        if not torch.cuda.is_available():
+            print("decode: no GPU visible", file=sys.stderr)
+            return 1
+        print(json.dumps(stress(a.op, a.steps, a.warmup)), flush=True)
+        return 0
     modes = tuple(m for m in a.modes.split(",") if m)
     if not modes or any(m not in MODES for m in modes):
         print(f"decode: --modes must name some of {MODES}", file=sys.stderr)

@@ -11,10 +11,12 @@ and not the host's submission (cq_pool_timing).  The read ceiling is
 cq_read_ceiling over an equally cold pool of the same bytes, same caliber.
 
 Usage: python -m cudalab_amd.evaluator.sweep [--steps K] [--json FILE]
-           [--ops int4gemv,qgemv,gemv] [--modes streaming,hot]
+           [--ops int4gemv,qgemv,gemv] [--modes streaming,hot,misaligned]
            [--shapes NxK,NxK...] [--variant OP=V1,V2 ...]
 Other shapes (e.g. Llama-70B's 8192x28672) and several variants per
 operator (e.g. the incumbent against *_lds_tiled) time the same way.
+"misaligned" is the streaming pool with W and x moved off their 16-byte
+alignment (the scalar fallback, bit-identical to *_baseline).
 """
 from __future__ import annotations
 
@@ -46,19 +48,47 @@ def algorithmic_bytes(op: str, N: int, K: int) -> int:
     return q8_bytes(N, K)
 
 
+MODES = ("streaming", "hot", "misaligned")
+
+
+def offset_copy(t: torch.Tensor, offset_bytes: int) -> torch.Tensor:
+    """The same values at a base address `offset_bytes` past a 16-byte
+    boundary (a view into a slightly larger byte buffer)."""
+    n = t.numel() * t.element_size()
+    flat = torch.empty(n + 64, dtype=torch.uint8, device=t.device)
+    view = flat[offset_bytes:offset_bytes + n].view(t.dtype).view_as(t)
+    view.copy_(t)
+    return view
+
+
 def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
     """Input sets drawn on the device: a pool of more than 512 MiB of
-    distinct sets for "streaming", one set for "hot".  INT4/INT8 sets are
-    (W, scale, x, out); FP16 sets are (W, x, out)."""
+    distinct sets for "streaming" and "misaligned", one set for "hot".
+    INT4/INT8 sets are (W, scale, x, out); FP16 sets are (W, x, out).
+    "misaligned" moves W one byte (INT4/INT8; two for FP16) and x two bytes
+    off their 16-byte alignment, the measurement plan's misaligned case:
+    every call then runs the scalar kernel, as the reference's did."""
     if op == "int4gemv":
         from ..operators.int4gemv import device_random_set
     elif op == "gemv":
         from ..operators.gemv import device_random_set
     else:
         from ..operators.qgemv import device_random_set
+    if mode not in MODES:
+        raise ValueError(f"unknown mode {mode!r} (one of {MODES})")
     nbytes = algorithmic_bytes(op, N, K)
-    n = cold_pool_sets(nbytes) if mode == "streaming" else 1
-    return [device_random_set(N, K, seed + 100000 + i) for i in range(n)], nbytes
+    n = cold_pool_sets(nbytes) if mode != "hot" else 1
+    sets = []
+    for i in range(n):
+        st = device_random_set(N, K, seed + 100000 + i)
+        if mode == "misaligned":
+            w_off = 2 if op == "gemv" else 1
+            xi = 1 if op == "gemv" else 2
+            st = tuple(offset_copy(t, w_off) if j == 0 else
+                       offset_copy(t, 2) if j == xi else t
+                       for j, t in enumerate(st))
+        sets.append(st)
+    return sets, nbytes
 
 
 def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
@@ -150,7 +180,8 @@ def main(argv=None) -> int:
     ap.add_argument("--shapes", default=None,
                     help='N x K list, e.g. "8192x28672,4096x4096" (default: the '
                          "five bench shapes)")
-    ap.add_argument("--modes", default="streaming,hot")
+    ap.add_argument("--modes", default="streaming,hot",
+                    help="comma-separated subset of " + ",".join(MODES))
     ap.add_argument("--variant", action="append", default=[], metavar="OP=V1,V2",
                     help="variants to time for an op (default: its incumbent)")
     ap.add_argument("--no-ceiling", action="store_true",
@@ -175,7 +206,7 @@ def main(argv=None) -> int:
         print("sweep: --shapes takes NxK,NxK... and --variant OP=V1,V2", file=sys.stderr)
         return 2
     modes = tuple(m for m in a.modes.split(",") if m)
-    if (any(len(sh) != 2 for sh in shapes) or any(m not in ("streaming", "hot") for m in modes)
+    if (any(len(sh) != 2 for sh in shapes) or any(m not in MODES for m in modes)
             or any(op not in OPS for op in variants)):
         print("sweep: bad --shapes, --modes or --variant", file=sys.stderr)
         return 2

@@ -129,8 +129,32 @@ def test_sweep_options(monkeypatch, capsys):
     assert sweep.main(["--shapes", "8192x28672,4096x4096"]) == 1     # parsed, no GPU
     assert sweep.main(["--variant", "int4gemv=int4gemv_cdna4,int4gemv_lds_tiled",
                        "--modes", "streaming"]) == 1
+    assert sweep.main(["--modes", "misaligned,streaming"]) == 1
     for bad in (["--shapes", "8x8x8"], ["--shapes", "8xq"], ["--modes", "warm"],
                 ["--variant", "softmax=x"], ["--variant", "int4gemv"], ["--ops", "rmsnorm"]):
         assert sweep.main(bad) == 2, bad
     err = capsys.readouterr().err
     assert "no GPU visible" in err and "--shapes" in err
+
+
+def test_sweep_misaligned_sets_keep_values_off_alignment():
+    """The misaligned mode's copies hold the same values at a base address
+    1 (W) or 2 (x) bytes past a 16-byte boundary."""
+    import torch
+    from cudalab_amd.evaluator.sweep import offset_copy
+    for dtype, off in ((torch.uint8, 1), (torch.int8, 1), (torch.float16, 2)):
+        t = torch.arange(48).to(dtype).view(3, 16)
+        v = offset_copy(t, off)
+        assert v.data_ptr() % 16 == off and v.is_contiguous()
+        assert torch.equal(v, t) and v.shape == t.shape and v.dtype == dtype
+
+
+def test_decode_stress_option(monkeypatch, capsys):
+    """--stress is parsed and needs a GPU; the sequence is the measurement
+    plan's: the 7B MLP pair, then four 4096^2 projections."""
+    import torch
+    from cudalab_amd import decode
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert decode.main(["--stress", "--op", "qgemv"]) == 1
+    assert "no GPU visible" in capsys.readouterr().err
+    assert decode.STRESS_SHAPES == ((11008, 4096), (4096, 11008)) + ((4096, 4096),) * 4

@@ -132,9 +132,11 @@ def _misaligned(t, offset_bytes):
     return view
 
 
-@pytest.mark.parametrize("woff,xoff", [(2, 0), (0, 2), (2, 2)])
+@pytest.mark.parametrize("woff,xoff", [(2, 0), (0, 2), (2, 2), (1, 0), (1, 2)])
 def test_misaligned_operands_exact(ext4, ext8, extg, woff, xoff):
-    """Operands off a 16-byte boundary take the scalar kernel; still exact."""
+    """Operands off a 16-byte boundary take the scalar kernel; still exact.
+    Odd weight offsets (the byte-wide INT4/INT8 weights, the reference's
+    +1 B case) are skipped for the FP16 GEMV, whose weights are 2-byte."""
     wp, s, x = _int4_exact(300, 4096, seed=1)
     want = orc.expect_exact_w4(_np(wp), _np(s), _np(x))
     wpm, xm = _misaligned(wp, woff), _misaligned(x, xoff)
@@ -146,6 +148,8 @@ def test_misaligned_operands_exact(ext4, ext8, extg, woff, xoff):
     announce(f"qgemv exact misaligned w+{woff} x+{xoff}")
     _same_bits(ext8.forward("qgemv_cdna4", _misaligned(wq, woff), s8, _misaligned(x8, xoff)),
                want8, "int8 misaligned")
+    if woff % 2:
+        return
     W, xg = _gemv_exact(300, 4096, torch.float16, seed=3)
     wantg = orc.expect_exact_gemv(_np(W), _np(xg))
     announce(f"gemv exact misaligned w+{woff} x+{xoff}")
