@@ -1,8 +1,10 @@
 // Host-only exercise of the C ABI (include/cdnaqgemv.h) under AddressSanitizer
 // and UndefinedBehaviorSanitizer: every argument check, the variant and
 // alias lists (with short buffers), the overlap checks of single and grouped
-// calls (5000 problems), the quantizer and timing argument checks, and
-// describe over every operator and size class.  Nothing here launches a
+// calls (5000 problems), the quantizer and timing argument checks,
+// describe over every operator and size class, and prepared launches
+// (cq_prepare over every operator; cq_launch_prepared only on records it
+// refuses).  Nothing here launches a
 // kernel or touches a GPU: every call fails its host-side checks first or
 // only plans.  Built and run by tests/test_host_sanitizers_cpu.py.
 #include "cdnaqgemv.h"
@@ -64,6 +66,24 @@ int main() {
                 cq_describe_launch(op, v, n, k, (const void*)0x1000, (const void*)0x2000, buf, 5);
             }
     cq_vec_contract_ok(CQ_OP_INT4GEMV, P, P, 128);
+    // prepared launches: checks, plans and records only; the launch entry
+    // point is only handed records it must refuse
+    cq_prepared_t rec;
+    for (int op : {CQ_OP_INT4GEMV, CQ_OP_QGEMV, CQ_OP_GEMV_F16, CQ_OP_GEMV_F32})
+        for (int64_t k : {16, 128, 4096, 28672}) {
+            const char* v = op == CQ_OP_INT4GEMV ? "int4gemv_cdna4" : op == CQ_OP_QGEMV ? "qgemv_cdna4" : "gemv_cdna4";
+            cq_prepare(op, v, (const void*)0x10000000, (const void*)0x20000000, (const void*)0x30000000,
+                       (void*)0x40000000, 4096, k, &rec);
+        }
+    cq_prepare(CQ_OP_INT4GEMV, "nope", P, P, P, Y, 8, 128, &rec);
+    cq_prepare(CQ_OP_INT4GEMV, "int4gemv_cdna4", P, P, P, Y, 8, 128, nullptr);
+    cq_launch_prepared(nullptr, nullptr);
+    cq_launch_prepared(&rec, nullptr);                 // zeroed by the failed prepare
+    cq_prepare(CQ_OP_QGEMV, "qgemv_cdna4", (const void*)0x10000000, (const void*)0x20000000,
+               (const void*)0x30000000, (void*)0x40000000, 64, 64, &rec);
+    rec.opaque[3] ^= 4;                                 // damaged: refused by its seal
+    cq_launch_prepared(&rec, nullptr);
+    std::printf("prepared: %s\n", cq_last_error());
     std::printf("version %s\ndone\n", cq_version());
     return 0;
 }

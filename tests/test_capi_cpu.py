@@ -281,6 +281,62 @@ def test_argument_errors_without_launch():
         assert st == _capi.CQ_ERR_INVALID_ARG and "grid must be" in _capi.last_error()
 
 
+def _prepare(lib, op, variant, w, s, x, y, n, k):
+    rec = _capi.CqPrepared()
+    for i in range(12):
+        rec.opaque[i] = 0xA5A5A5A5A5A5A5A5          # must be overwritten either way
+    st = lib.cq_prepare(op, variant, w, s, x, y, n, k, ctypes.byref(rec))
+    return st, rec
+
+
+def test_prepare_checks_like_the_direct_call_and_launches_nothing():
+    """cq_prepare runs the direct call's checks with the same statuses and
+    messages and zeroes the record on failure; on success it fills a
+    deterministic record (same arguments, same bytes).  It makes no GPU
+    call, so this runs on the CPU with fake, disjoint device addresses."""
+    lib = _capi.load()
+    W, S, X, Y = 0x10000000, 0x20000000, 0x30000000, 0x40000000
+    for args, status, words in (
+            ((0, b"no_such_variant", W, S, X, Y, 8, 128), _capi.CQ_ERR_UNKNOWN_VARIANT, "no_such_variant"),
+            ((0, b"int4gemv_cdna4", W, S, X, Y, 8, 100), _capi.CQ_ERR_INVALID_ARG, "128"),
+            ((0, b"int4gemv_cdna4", None, S, X, Y, 8, 128), _capi.CQ_ERR_INVALID_ARG, "null"),
+            ((0, b"int4gemv_cdna4", W, S, X, X, 8, 128), _capi.CQ_ERR_INVALID_ARG, "overlaps"),
+            ((1, b"qgemv_cdna4", W, S, X, Y, 0, 16), _capi.CQ_ERR_INVALID_ARG, "n must be"),
+            ((7, b"int4gemv_cdna4", W, S, X, Y, 8, 128), _capi.CQ_ERR_INVALID_ARG, "operator")):
+        st, rec = _prepare(lib, *args)
+        assert st == status and words in _capi.last_error(), (args, st, _capi.last_error())
+        assert list(rec.opaque) == [0] * 12, args
+    assert lib.cq_prepare(0, b"int4gemv_cdna4", W, S, X, Y, 8, 128, None) == _capi.CQ_ERR_INVALID_ARG
+    st1, r1 = _prepare(lib, 0, b"int4gemv_cdna4", W, S, X, Y, 4096, 4096)
+    st2, r2 = _prepare(lib, 0, b"int4gemv_cdna4", W, S, X, Y, 4096, 4096)
+    st3, r3 = _prepare(lib, 0, b"int4gemv_lds_r2", W, S, X, Y, 4096, 4096)
+    st4, r4 = _prepare(lib, 0, b"int4gemv_rowtile4_hx", W, S, X, Y, 4096, 4096)  # alias
+    assert st1 == st2 == st3 == st4 == _capi.CQ_OK, _capi.last_error()
+    assert list(r1.opaque) == list(r2.opaque) == list(r4.opaque)
+    assert list(r1.opaque) != list(r3.opaque) and any(r1.opaque)
+    # the FP16/FP32 GEMV ignores the scale pointer, as cq_gemv does
+    sa, ga = _prepare(lib, _capi.CQ_OP_GEMV_F16, b"gemv_cdna4", W, None, X, Y, 64, 64)
+    sb, gb = _prepare(lib, _capi.CQ_OP_GEMV_F16, b"gemv_cdna4", W, S, X, Y, 64, 64)
+    assert sa == sb == _capi.CQ_OK and list(ga.opaque) == list(gb.opaque)
+
+
+def test_launch_prepared_refuses_records_prepare_did_not_fill():
+    """A zeroed, damaged or null record is refused before any GPU call."""
+    lib = _capi.load()
+    assert lib.cq_launch_prepared(None, None) == _capi.CQ_ERR_INVALID_ARG
+    zero = _capi.CqPrepared()
+    assert lib.cq_launch_prepared(ctypes.addressof(zero), None) == _capi.CQ_ERR_INVALID_ARG
+    assert "cq_prepare" in _capi.last_error()
+    st, rec = _prepare(lib, 0, b"int4gemv_cdna4", 0x10000000, 0x20000000,
+                       0x30000000, 0x40000000, 4096, 4096)
+    assert st == _capi.CQ_OK
+    for word in range(11):                       # every word the seal covers
+        bad = _capi.CqPrepared()
+        ctypes.memmove(ctypes.byref(bad), ctypes.byref(rec), ctypes.sizeof(rec))
+        bad.opaque[word] ^= 1 << (word % 64)
+        assert lib.cq_launch_prepared(ctypes.addressof(bad), None) == _capi.CQ_ERR_INVALID_ARG, word
+
+
 def _disjoint_problems(count, n=8):
     """Problems with non-overlapping fake device addresses (never launched:
     every call below fails its argument checks first)."""
