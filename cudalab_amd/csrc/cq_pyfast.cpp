@@ -118,6 +118,9 @@ public:
         for (size_t i = 0; i < names_.size(); ++i)
             ids_.emplace(std::string_view(names_[i]), static_cast<int32_t>(i));
     }
+    // ids_ views the strings of names_: a copy would view the original's
+    Launcher(const Launcher&) = delete;
+    Launcher& operator=(const Launcher&) = delete;
 
     // ---- the metadata rule, for tests (no launch, no cache) ----
     bool accepts(const at::Tensor& w, const at::Tensor& scale, const at::Tensor& x,
