@@ -2,7 +2,9 @@
 // Python checks the tensors of a forward / forward_into call on their
 // metadata, finds the launch in a cache of prepared launches (cq_prepare,
 // keyed by variant, operand addresses and sizes) and enqueues it on the
-// current HIP stream of the operands' device (cq_launch_prepared).
+// current HIP stream of the operands' device (cq_launch_prepared).  Grouped
+// calls (forward_grouped) take the same checks per problem and go to the
+// library's grouped entry point directly.
 //
 // The reference's bindings do their checks and the launch in C++ as well
 // (kernels/int4gemv/bindings.cpp:60-176, kernels/qgemv/bindings.cpp:65-173,
@@ -50,6 +52,7 @@ using PrepareFn = int (*)(int, const char*, const void*, const void*, const void
                           void*, int64_t, int64_t, cq_prepared_t*);
 using LaunchFn = int (*)(const cq_prepared_t*, void*);
 using ErrorFn = const char* (*)();
+using GroupedFn = int (*)(const char*, const cq_gemv_problem_t*, int64_t, int64_t, void*);
 
 enum Kind { kInt4 = 0, kQ8 = 1, kGemv = 2 };
 
@@ -105,11 +108,13 @@ bool same_device(const at::Tensor& w, std::initializer_list<const at::Tensor*> r
 class Launcher {
 public:
     Launcher(int kind, const std::vector<std::string>& names, uintptr_t prepare,
-             uintptr_t launch, uintptr_t last_error, int64_t capacity)
+             uintptr_t launch, uintptr_t last_error, int64_t capacity,
+             uintptr_t grouped)
         : kind_(kind),
           prepare_(reinterpret_cast<PrepareFn>(prepare)),
           launch_(reinterpret_cast<LaunchFn>(launch)),
           last_error_(reinterpret_cast<ErrorFn>(last_error)),
+          grouped_(reinterpret_cast<GroupedFn>(grouped)),
           capacity_(capacity < 1 ? 1 : static_cast<size_t>(capacity)),
           names_(names) {
         if (kind < kInt4 || kind > kGemv) throw std::invalid_argument("unknown operator kind");
@@ -178,6 +183,57 @@ public:
         at::Tensor Y = at::empty({W.size(0)}, W.options());
         if (!run(vid, W, nullptr, X, Y)) return py::none();
         return py::cast(Y);
+    }
+
+    // ---- INT4 / INT8 grouped calls ----
+    // `problems` must be a list or tuple (any other iterable is left
+    // unconsumed for the checked path) of 4-item lists or tuples of
+    // tensors, each accepted by the forward_into rule, all with one K and
+    // on one device.  The library's grouped entry point then runs its own
+    // checks (overlaps included); a refusal there is "not taken" too, so
+    // the checked path raises it with the reference-style message.
+    bool grouped(py::handle variant, py::handle problems) {
+        const int32_t vid = variant_id(variant);
+        if (vid < 0 || kind_ == kGemv || grouped_ == nullptr) return false;
+        PyObject* seq = problems.ptr();
+        if (!PyList_Check(seq) && !PyTuple_Check(seq)) return false;
+        const Py_ssize_t count = PySequence_Fast_GET_SIZE(seq);
+        if (count < 1) return false;
+        std::vector<cq_gemv_problem_t> probs(static_cast<size_t>(count));
+        int64_t k0 = 0;
+        c10::Device dev0(c10::DeviceType::CPU);
+        for (Py_ssize_t i = 0; i < count; ++i) {
+            PyObject* item = PySequence_Fast_GET_ITEM(seq, i);
+            if ((!PyTuple_Check(item) && !PyList_Check(item)) ||
+                PySequence_Fast_GET_SIZE(item) != 4)
+                return false;
+            PyObject** f = PySequence_Fast_ITEMS(item);
+            for (int j = 0; j < 4; ++j)
+                if (!THPVariable_Check(f[j])) return false;
+            const at::Tensor& W = THPVariable_Unpack(f[0]);
+            const at::Tensor& S = THPVariable_Unpack(f[1]);
+            const at::Tensor& X = THPVariable_Unpack(f[2]);
+            const at::Tensor& Y = THPVariable_Unpack(f[3]);
+            if (!quant_ok(W, S, X, &Y, true)) return false;
+            const int64_t k = kind_ == kInt4 ? 2 * W.size(1) : W.size(1);
+            if (i == 0) {
+                k0 = k;
+                dev0 = W.device();
+            } else if (k != k0 || W.device() != dev0) {
+                return false;
+            }
+            probs[static_cast<size_t>(i)] = {W.data_ptr(), S.data_ptr(), X.data_ptr(),
+                                             Y.data_ptr(), W.size(0)};
+        }
+        const hipStream_t stream = c10::hip::getCurrentHIPStream(dev0.index()).stream();
+        const int st = grouped_(names_[static_cast<size_t>(vid)].c_str(), probs.data(),
+                                static_cast<int64_t>(count), k0, stream);
+        if (st == CQ_OK) return true;
+        if (st == CQ_ERR_HIP)
+            throw std::runtime_error(std::string(kind_ == kInt4 ? "int4gemv" : "qgemv") +
+                                     " grouped launch failed (status " + std::to_string(st) +
+                                     "): " + last_error_());
+        return false;
     }
 
     bool knows(py::handle variant) const { return variant_id(variant) >= 0; }
@@ -273,6 +329,7 @@ private:
     PrepareFn prepare_;
     LaunchFn launch_;
     ErrorFn last_error_;
+    GroupedFn grouped_;
     size_t capacity_;
     std::vector<std::string> names_;
     std::unordered_map<std::string_view, int32_t> ids_;
@@ -286,15 +343,16 @@ PYBIND11_MODULE(_cqfast, m) {
     m.attr("src_hash") = CQ_SRC_HASH;
     py::class_<Launcher>(m, "Launcher")
         .def(py::init<int, const std::vector<std::string>&, uintptr_t, uintptr_t,
-                      uintptr_t, int64_t>(),
+                      uintptr_t, int64_t, uintptr_t>(),
              py::arg("kind"), py::arg("names"), py::arg("prepare"), py::arg("launch"),
-             py::arg("last_error"), py::arg("capacity"))
+             py::arg("last_error"), py::arg("capacity"), py::arg("grouped") = 0)
         .def("accepts", &Launcher::accepts)
         .def("gemv_accepts", &Launcher::gemv_accepts)
         .def("into", &Launcher::into)
         .def("forward", &Launcher::forward)
         .def("gemv_into", &Launcher::gemv_into)
         .def("gemv_forward", &Launcher::gemv_forward)
+        .def("grouped", &Launcher::grouped)
         .def("knows", &Launcher::knows)
         .def("cached", &Launcher::cached)
         .def("clear", &Launcher::clear);

@@ -268,10 +268,9 @@ def run(op: str = "int4gemv", layers: int | None = None, steps: int = 20,
            "bytes_per_step": m.bytes_per_step,
            "launches_per_layer": {"sequential": 7, "grouped": 4, "graph": 4},
            "note": "sequential and grouped include the Python API path of "
-                   "every call (forward_into: the checked-once fast path; "
-                   "forward_grouped: checks in Python, one ctypes launch); "
-                   "graph replays the grouped step's launches from one HIP "
-                   "graph"}
+                   "every call (forward_into and forward_grouped through "
+                   "the checked-once fast path); graph replays the grouped "
+                   "step's launches from one HIP graph"}
     fns = {"sequential": m.step_sequential, "grouped": m.step_grouped,
            "graph": graph.replay if graph is not None else None}
     for mode in modes:

@@ -16,6 +16,7 @@ First the floor: the library's own C loop enqueueing the same launch
 Paths (INT4 int4gemv_cdna4 at N x K, then FP16 gemv_cdna4 and torch.mv):
   forward_into       the public call (the fast path of csrc/cq_pyfast.cpp)
   forward            the same, allocating the output
+  forward_grouped    three problems of the shape in one grouped launch
   checked path       variant lookup, the metadata checks in the reference's
                      order and the ctypes launch (what forward_into runs
                      when the fast path declines)
@@ -125,6 +126,8 @@ def run(n: int = 4096, k: int = 4096, calls: int = 1000, reps: int = 7) -> dict:
                                ctypes.byref(prepared)), "cq_prepare")
     addr = ctypes.addressof(prepared)
 
+    group = [(W, s, x, out)] + [device_random_set(n, k, 2 + i) for i in range(2)]
+
     def checked():
         ext4._lookup(v)
         ext4._validate_inputs(W, s, x)
@@ -134,6 +137,7 @@ def run(n: int = 4096, k: int = 4096, calls: int = 1000, reps: int = 7) -> dict:
     paths = {
         "forward_into": lambda: ext4.forward_into(v, W, s, x, out),
         "forward": lambda: ext4.forward(v, W, s, x),
+        "forward_grouped (3 problems)": lambda: ext4.forward_grouped(v, group),
         "checked path": checked,
         "cq_int4gemv (ctypes)": lambda: lib.cq_int4gemv(vb, *ptrs, n, k, stream),
         "cq_launch_prepared (ctypes)": lambda: lib.cq_launch_prepared(addr, stream),

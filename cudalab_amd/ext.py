@@ -58,11 +58,16 @@ FAST_CACHE_ENTRIES = 4096
 _FAST_KIND = {"int4gemv": 0, "qgemv": 1, "gemv": 2}
 
 
+_GROUPED_ENTRY = {"int4gemv": "cq_int4gemv_grouped", "qgemv": "cq_qgemv_grouped"}
+
+
 def _fast_launcher(op: str, names: list[str]):
+    grouped = _GROUPED_ENTRY.get(op)
     return _capi.fast_module().Launcher(
         _FAST_KIND[op], names, _capi.entry_address("cq_prepare"),
         _capi.entry_address("cq_launch_prepared"),
-        _capi.entry_address("cq_last_error"), FAST_CACHE_ENTRIES)
+        _capi.entry_address("cq_last_error"), FAST_CACHE_ENTRIES,
+        _capi.entry_address(grouped) if grouped else 0)
 
 
 def _fail(msg: str) -> None:
@@ -203,6 +208,8 @@ class _OpExt:
         bit-identical to forward_into(variant, W, scale, x, out).  No
         counterpart in the reference (its modules launch one problem at a
         time)."""
+        if self._fast.grouped(variant, problems):
+            return
         self._lookup(variant)
         problems = list(problems)
         if not problems:

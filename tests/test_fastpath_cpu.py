@@ -164,3 +164,25 @@ def test_knows_exactly_the_names_the_checked_path_accepts(exts):
         for other in ("", "int4gemv", "gemv_cdna4 ", "qgemv_cdna4x"):
             assert not e._fast.knows(other), (op, other)
         assert not e._fast.knows(None)
+
+
+def test_grouped_not_taken_without_launching(exts):
+    """The grouped fast path takes only lists or tuples of 4-item problems
+    of GPU tensors; anything else is "not taken" -- and an iterator is left
+    unconsumed for the checked path."""
+    b = _int4_base()
+    prob = (b["W"], b["s"], b["x"], b["out"])
+    fast = exts["int4gemv"]._fast
+    assert fast.grouped("int4gemv_cdna4", [prob, prob]) is False     # CPU tensors
+    assert fast.grouped("int4gemv_cdna4", []) is False
+    assert fast.grouped("int4gemv_cdna4", [prob[:3]]) is False
+    assert fast.grouped("int4gemv_cdna4", [list(prob) + [None]]) is False
+    assert fast.grouped("int4gemv_cdna4", [(None,) * 4]) is False
+    assert fast.grouped("int4gemv_cdna4", prob[0]) is False
+    assert fast.grouped("no_such_variant", [prob]) is False
+    it = iter([prob])
+    assert fast.grouped("int4gemv_cdna4", it) is False
+    assert next(it) is prob                                        # not consumed
+    assert exts["gemv"]._fast.grouped("gemv_cdna4", [prob]) is False
+    with pytest.raises(RuntimeError, match="CUDA 张量"):
+        exts["int4gemv"].forward_grouped("int4gemv_cdna4", iter([prob]))

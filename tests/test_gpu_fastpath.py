@@ -182,3 +182,32 @@ def test_prepared_record_c_api(ext4):
     assert lib.cq_launch_prepared(ctypes.addressof(rec), stream) == _capi.CQ_ERR_INVALID_ARG
     assert "cq_prepare" in _capi.last_error()
     assert E.FAST_CACHE_ENTRIES >= 1024
+
+
+@pytest.mark.parametrize("op", ["int4gemv", "qgemv"])
+def test_grouped_fast_path_matches_single_calls(ext4, ext8, op):
+    """forward_grouped through the fast path: every output bit-identical to
+    forward_into of its problem; a mixed-K group is declined and raises the
+    checked path's message; an iterator still works (checked path)."""
+    e, make = (ext4, _int4) if op == "int4gemv" else (ext8, _q8)
+    v = "int4gemv_cdna4" if op == "int4gemv" else "qgemv_cdna4"
+    probs = [make(N, 4096, seed=40 + N) for N in (4096, 1024, 1024, 300)]
+    outs = [torch.full((W.size(0),), float("nan"), dtype=torch.float16, device="cuda")
+            for W, _, _ in probs]
+    announce(f"grouped fast path {op}")
+    assert e._fast.grouped(v, [(W, s, x, o) for (W, s, x), o in zip(probs, outs)]) is True
+    for (W, s, x), o in zip(probs, outs):
+        want = torch.empty_like(o)
+        e._launch(v, W, s, x, want)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(o), _bits(want))
+    other = make(64, 2048, seed=9)
+    mixed = [(*probs[0], outs[0]), (*other, torch.empty(64, dtype=torch.float16, device="cuda"))]
+    assert e._fast.grouped(v, mixed) is False
+    with pytest.raises(RuntimeError, match="相同的 K"):
+        e.forward_grouped(v, mixed)
+    outs2 = [torch.empty_like(o) for o in outs]
+    e.forward_grouped(v, ((W, s, x, o) for (W, s, x), o in zip(probs, outs2)))
+    torch.cuda.synchronize()
+    for o, o2 in zip(outs, outs2):
+        assert torch.equal(_bits(o), _bits(o2))
