@@ -14,15 +14,17 @@ the CPU test suite can reach them; the C layer receives plain pointers and
 sizes and picks the kernel (vectorized or scalar fallback) from alignment.
 Launches go on the current torch stream of the weights' device.
 
-`forward` and `forward_into` first offer the call to the fast path
-(csrc/cq_pyfast.cpp): one C++ call that applies the same acceptance rule to
-the tensors' metadata, looks the launch up in a cache of launches prepared
-once by cq_prepare (keyed by variant, operand addresses and sizes, so a
-cached launch is exactly what preparing again would give) and enqueues it.
-It launches nothing for a call it does not accept, and the checked path
-below then runs and raises in the reference's order.  On MI355X this took
-an INT4 forward_into from 7.0-8.2 us of host time to 3.0-3.2 us, within
-0.1-0.7 us of hipLaunchKernel itself (2.2-3.1 us depending on the host).
+`forward`, `forward_into` and `forward_grouped` first offer the call to the
+fast path (csrc/cq_pyfast.cpp): one C++ call that applies the same
+acceptance rule to the tensors' metadata, looks the launch up in a cache of
+launches prepared once by cq_prepare (keyed by variant, operand addresses
+and sizes, so a cached launch is exactly what preparing again would give)
+and enqueues it; a grouped call goes to the library's grouped entry point
+directly.  It launches nothing for a call it does not accept, and the
+checked path below then runs and raises in the reference's order.  On
+MI355X this took an INT4 forward_into from 7.0-8.2 us of host time to
+3.0-3.2 us, within 0.1-0.7 us of hipLaunchKernel itself (2.2-3.1 us
+depending on the host).
 """
 from __future__ import annotations
 
