@@ -136,12 +136,23 @@ def test_prepared_launch_follows_the_current_stream(ext4):
     side = torch.cuda.Stream()
     out = torch.full_like(want, float("nan"))
     announce("fast path on a side stream")
+    peek = torch.cuda.Stream()
+    host = torch.empty(out.shape, dtype=out.dtype, pin_memory=True)
     torch.cuda.synchronize()
     with torch.cuda.stream(side):
-        torch.cuda._sleep(2_000_000)              # hold the side stream busy
+        torch.cuda._sleep(100_000_000)            # hold the side stream busy (tens of ms)
         ext4.forward_into("int4gemv_cdna4", W, s, x, out)
         done = torch.cuda.Event()
         done.record(side)
+    # a third stream reads `out` while the side stream still waits: the
+    # launch queued behind the wait has not run, so `out` still holds NaN
+    with torch.cuda.stream(peek):
+        host.copy_(out, non_blocking=True)
+        peeked = torch.cuda.Event()
+        peeked.record(peek)
+    peeked.synchronize()
+    assert not done.query(), "the side stream's wait ended before the peek"
+    assert torch.isnan(host.float()).all()
     done.synchronize()
     assert torch.equal(_bits(out), _bits(want))
     announce("fast path under graph capture")
