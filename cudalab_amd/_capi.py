@@ -114,6 +114,13 @@ SIGNATURES = {
     "cq_launch_floor": (ctypes.c_int, [_i64, ctypes.c_int, _vp, _vp, _i64,
                                        ctypes.c_double, ctypes.c_double, _i64,
                                        ctypes.POINTER(ctypes.c_double)]),
+    "cq_int4_timeline": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp),
+                                        ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                        ctypes.POINTER(_vp), _i64, _i64, _i64, _vp,
+                                        _i64, ctypes.c_double, ctypes.c_double,
+                                        _i64, _vp, _i64, ctypes.POINTER(_i64),
+                                        ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_double)]),
     "cq_variants": (ctypes.c_int, [ctypes.c_int, ctypes.c_int,
                                    ctypes.c_char_p, ctypes.c_size_t]),
     "cq_vec_contract_ok": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64]),

@@ -698,6 +698,62 @@ int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
     return timed_window(go, s, win, nullptr, total_us, nullptr);
 }
 
+int cq_int4_timeline(const char* variant, const void* const* w,
+                     const void* const* scale, const void* const* x,
+                     void* const* y, int64_t n_sets, int64_t n, int64_t k,
+                     void* stream, int64_t warmup, double burn_ms,
+                     double delay_us, int64_t n_launches, uint64_t* stamps,
+                     int64_t stamps_words, int64_t* waves_out,
+                     double* ticks_per_us, double* total_us) {
+    g_last_error.clear();
+    if (w == nullptr || scale == nullptr || x == nullptr || y == nullptr ||
+        stamps == nullptr || waves_out == nullptr || ticks_per_us == nullptr ||
+        total_us == nullptr)
+        return fail(CQ_ERR_INVALID_ARG, "null argument");
+    if (n_sets < 1) return fail(CQ_ERR_INVALID_ARG, "n_sets must be >= 1");
+    const Window win{warmup, burn_ms, delay_us, n_launches};
+    int st = check_window(win);
+    if (st != CQ_OK) return st;
+    std::vector<cq::Plan> plans(static_cast<size_t>(n_sets));
+    const Variant* v = nullptr;
+    for (int64_t i = 0; i < n_sets; ++i) {
+        st = check_launch(CQ_OP_INT4GEMV, variant, &v, w[i], scale[i], x[i], y[i], n, k);
+        if (st != CQ_OK) return st;
+        cq::Plan& p = plans[static_cast<size_t>(i)];
+        p = make_plan(CQ_OP_INT4GEMV, *v, n, k, w[i], x[i]);
+        if (p.kind != cq::kLds)
+            return fail(CQ_ERR_INVALID_ARG,
+                        std::string("the timeline covers the LDS kernel; ") + v->name +
+                            " plans another kernel for set " + std::to_string(i));
+        if (p.grid != plans[0].grid || p.block != plans[0].block)
+            return fail(CQ_ERR_INVALID_ARG, "the sets' plans differ in launch shape");
+    }
+    const int64_t waves = plans[0].grid * (plans[0].block / 64);
+    if (n_launches > (INT64_MAX / 8) / waves || stamps_words < n_launches * waves * 8)
+        return fail(CQ_ERR_INVALID_ARG,
+                    "stamps holds " + std::to_string(stamps_words) + " words; " +
+                        std::to_string(n_launches) + " launches of " +
+                        std::to_string(waves) + " waves need 8 per wave");
+    int dev = 0, khz = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    if (khz <= 0) return fail(CQ_ERR_HIP, "the device reports no wall clock rate");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto go = [&](int64_t i, hipEvent_t, hipEvent_t) {
+        const size_t si = static_cast<size_t>(i % n_sets);
+        uint64_t* slot = stamps + (i % n_launches) * waves * 8;
+        return cq::launch_int4_stamped(plans[si], w[si], scale[si], x[si], y[si], n, k,
+                                       slot, s);
+    };
+    st = timed_window(go, s, win, nullptr, total_us, nullptr);
+    if (st != CQ_OK) return st;
+    *waves_out = waves;
+    *ticks_per_us = static_cast<double>(khz) / 1000.0;
+    return CQ_OK;
+}
+
 int cq_variants(int op, int which, char* buf, size_t cap) {
     g_last_error.clear();
     if (!valid_op(op))

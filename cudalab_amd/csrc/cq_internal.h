@@ -77,6 +77,13 @@ hipError_t launch_q8(const Plan& plan, const void* w, const void* scale,
                      const void* x, void* y, int64_t n, int64_t k,
                      hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
 
+// The timeline diagnostic: one launch of an INT4 LDS plan (kind kLds only)
+// through the stamped copy of its kernel, which writes 8 words per wave to
+// `stamps` (waves = grid * block / 64).
+hipError_t launch_int4_stamped(const Plan& plan, const void* w, const void* scale,
+                               const void* x, void* y, int64_t n, int64_t k,
+                               uint64_t* stamps, hipStream_t stream);
+
 // Grouped launches: up to kMaxGroup independent problems of one k in one
 // launch of the LDS kernels.
 constexpr int kMaxGroup = 8;

@@ -383,15 +383,38 @@ __global__ __launch_bounds__(kBlock) void qgemv_wave_kernel(
 // scheduling barrier after the workgroup barrier keeps weight arithmetic
 // (and its waits) from being hoisted above it.
 
+// The timeline stamps pin their clock reads by data dependence, not by
+// scheduling fences (the compiler places pure arithmetic before the machine
+// scheduler sees a fence, and a full fence also held every LDS read of x
+// live at once, doubling the VGPRs at J = 6).  wall_clock_through(v) reads
+// the wall clock with `v` passed through as an operand it may modify: the
+// read waits for the arithmetic that produces v, and whatever uses v after
+// it waits for the read.  The read is a scalar memory instruction the
+// compiler does not track, so it waits for its own result before anything
+// else counts on the LGKM counter.
+__device__ __forceinline__ uint64_t wall_clock_through(float& v) {
+    uint64_t t;
+    asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(v));
+    return t;
+}
+
 // The rows of logical workgroup `blk` of one INT4 problem.  `xs` is the
 // workgroup's LDS: [4][CW*J + 1] re-paired x pieces, q-major.
-template <int CW, int J, int R, int NT>
+//
+// STAMP (the timeline diagnostic only; every GEMV instance has it false, and
+// then none of its code exists): lane 0 of each wave writes 8 words to
+// stamps[wave * 8 ..]: the 100 MHz wall clock at the wave's start, after the
+// x barrier, after its first chunk is summed, after its last chunk is
+// summed and after its y stores are issued; then the hardware CU id.
+template <int CW, int J, int R, int NT, bool STAMP = false>
 __device__ __forceinline__ void int4_lds_rows(
         const uint4* __restrict__ w,         // [n][nchunks] 16-byte chunks
         const uint16_t* __restrict__ scale,  // [n][nchunks/4]
         const uint4* __restrict__ x,         // [4*nchunks] 16-byte pieces
         uint16_t* __restrict__ y, int n, int nchunks, uint32_t blk,
-        uint4* __restrict__ xs) {
+        uint4* __restrict__ xs, uint64_t* __restrict__ stamps = nullptr) {
+    [[maybe_unused]] uint64_t ts[5] = {};
+    if constexpr (STAMP) ts[0] = wall_clock64();
     constexpr int SLOTS = 64 / CW;
     constexpr int S = CW * J + 1;                     // LDS plane stride
     constexpr int XPER = (4 * CW * J + NT - 1) / NT;  // x pieces per thread
@@ -457,6 +480,7 @@ __device__ __forceinline__ void int4_lds_rows(
     if (tid < 4) xs[tid * S + CW * J] = uint4{0, 0, 0, 0};
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (STAMP) ts[1] = wall_clock64();
     uint4 xp[J][4];
     const int xlast = clast < nchunks ? clast : CW * J;
 #pragma unroll
@@ -477,6 +501,10 @@ __device__ __forceinline__ void int4_lds_rows(
             const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z,
                                        wv[r][j].w};
             float d = 0.f;
+            if constexpr (STAMP) {
+                // the second chunk's sum starts after the first stamp
+                if (r * J + j == 1) asm volatile("" : "+v"(d) : "v"(acc));
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t u = words[q];
@@ -491,10 +519,28 @@ __device__ __forceinline__ void int4_lds_rows(
                 d = __builtin_amdgcn_fdot2(qd, as_f16x2(xp[j][q].w), d, false);
             }
             acc = __builtin_fmaf(h2f(sv[r][j]), d, acc);
+            if constexpr (STAMP) {
+                if (r == 0 && j == 0) ts[2] = wall_clock_through(acc);
+                if (r == R - 1 && j == J - 1) ts[3] = wall_clock_through(acc);
+            }
         }
         acc = segment_sum<CW>(acc);
         const int64_t row = row0 + SLOTS * r;
         if (col == CW - 1 && row < n) y[row] = f2h(acc);
+    }
+    if constexpr (STAMP) {
+        __builtin_amdgcn_sched_barrier(0);
+        ts[4] = wall_clock64();
+        if (lane == 0) {
+            const uint64_t wave = static_cast<uint64_t>(blk) * (NT >> 6) +
+                                  static_cast<uint64_t>(tid >> 6);
+            uint64_t* o = stamps + wave * 8;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) o[i] = ts[i];
+            o[5] = __smid();
+            o[6] = 0;
+            o[7] = 0;
+        }
     }
 }
 
@@ -619,6 +665,18 @@ __global__ __launch_bounds__(NT) void int4gemv_lds_kernel(
     extern __shared__ uint4 xs[];
     int4_lds_rows<CW, J, R, NT>(w, scale, x, y, n, nchunks,
                                 xcd_contiguous_block(), xs);
+}
+
+// The INT4 LDS kernel with the timeline stamps (diagnostic, cq_int4_timeline):
+// the same arithmetic and launch shape; `stamps` holds 8 words per wave.
+template <int CW, int J, int R, int NT>
+__global__ __launch_bounds__(NT) void int4gemv_lds_stamp_kernel(
+        const uint4* __restrict__ w, const uint16_t* __restrict__ scale,
+        const uint4* __restrict__ x, uint16_t* __restrict__ y, int n,
+        int nchunks, uint64_t* __restrict__ stamps) {
+    extern __shared__ uint4 xs[];
+    int4_lds_rows<CW, J, R, NT, true>(w, scale, x, y, n, nchunks,
+                                      xcd_contiguous_block(), xs, stamps);
 }
 
 template <int CW, int J, int R, int NT>
@@ -1227,6 +1285,19 @@ struct Q8Lds {
     }
 };
 
+using Int4StampFn = void (*)(const uint4*, const uint16_t*, const uint4*,
+                             uint16_t*, int, int, uint64_t*);
+template <int NT>
+struct Int4LdsStamp {
+    using Fn = Int4StampFn;
+    static constexpr int kMaxJ = kInt4MaxJ;
+    template <int CW, int J, int R>
+    static constexpr Fn get() {
+        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_stamp_kernel<CW, J, R, NT>;
+        else return nullptr;
+    }
+};
+
 using Int4GroupFn = void (*)(GroupArgs, int);
 using Q8GroupFn = void (*)(GroupArgs, int);
 
@@ -1549,6 +1620,20 @@ hipError_t launch_int4(const Plan& p, const void* w, const void* scale,
     Launch L;
     const hipError_t e = prepare_int4(p, w, scale, x, y, n, k, &L);
     return e != hipSuccess ? e : enqueue(L, stream, ev0, ev1);
+}
+
+hipError_t launch_int4_stamped(const Plan& p, const void* w, const void* scale,
+                               const void* x, void* y, int64_t n, int64_t k,
+                               uint64_t* stamps, hipStream_t stream) {
+    if (p.kind != kLds || !lds_chunks_ok(p, k / 32)) return hipErrorInvalidConfiguration;
+    const Int4StampFn fn = p.block == 512 ? instance<Int4LdsStamp<512>>(p.cw, p.j, p.r)
+                                          : instance<Int4LdsStamp<kBlock>>(p.cw, p.j, p.r);
+    if (fn == nullptr) return hipErrorInvalidConfiguration;
+    return launch(fn, p.grid, p.block, int4_lds_bytes(p.cw, p.j), stream, nullptr,
+                  nullptr, static_cast<const uint4*>(w),
+                  static_cast<const uint16_t*>(scale), static_cast<const uint4*>(x),
+                  static_cast<uint16_t*>(y), static_cast<int>(n),
+                  static_cast<int>(k / 32), stamps);
 }
 
 hipError_t launch_q8(const Plan& p, const void* w, const void* scale,

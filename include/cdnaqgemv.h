@@ -281,6 +281,31 @@ int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
                     int64_t n_launches, double* total_us);
 
 /*
+ * Wave timeline of the INT4 GEMV (a diagnostic; no counterpart in the
+ * reference: it shows where the time of one call goes).  The sets and the
+ * window are those of cq_pool_timing (op CQ_OP_INT4GEMV); every launch,
+ * untimed ones included, runs a copy of the LDS kernel that `variant` plans
+ * for (n, k) -- the same arithmetic, launch shape and y -- which stamps each
+ * of its `waves` waves (*waves_out = grid * block / 64).  Launch i writes 8
+ * words per wave at stamps[((i % n_launches) * waves + wave) * 8]: the wall
+ * clock at the wave's start, after its x barrier, after its first and its
+ * last weight chunk are summed, after its y stores are issued, then the
+ * wave's hardware CU id and two zero words.  Every slot is last written by
+ * one of the n_launches timed launches; their order follows from the
+ * stamps.  `stamps` is device memory of `stamps_words` (at least
+ * n_launches * waves * 8) 64-bit words.  *ticks_per_us is the clock's rate,
+ * *total_us the window's event time.  CQ_ERR_INVALID_ARG when a set's plan
+ * is not the LDS kernel (the scalar or K-tiled kernels are not covered).
+ */
+int cq_int4_timeline(const char* variant, const void* const* w,
+                     const void* const* scale, const void* const* x,
+                     void* const* y, int64_t n_sets, int64_t n, int64_t k,
+                     void* stream, int64_t warmup, double burn_ms,
+                     double delay_us, int64_t n_launches, uint64_t* stamps,
+                     int64_t stamps_words, int64_t* waves_out,
+                     double* ticks_per_us, double* total_us);
+
+/*
  * Variant names of `op`, sorted, '\n'-separated, NUL-terminated, written to
  * buf (capacity cap).  which = CQ_LIST_NORMAL (dispatchable),
  * CQ_LIST_ALL (also quarantined), CQ_LIST_QUARANTINED, or CQ_LIST_ALIASES

@@ -281,6 +281,42 @@ def test_argument_errors_without_launch():
         assert st == _capi.CQ_ERR_INVALID_ARG and "grid must be" in _capi.last_error()
 
 
+def test_timeline_refuses_before_any_launch():
+    """cq_int4_timeline's refusals come from host checks alone (fake,
+    disjoint device addresses; nothing is launched): null arguments, a set
+    whose plan is not the LDS kernel (a misaligned W takes the scalar
+    kernel), a stamp buffer too small."""
+    lib = _capi.load()
+    VP1 = ctypes.c_void_p * 1
+    w, s, x, y = VP1(0x10000000), VP1(0x20000000), VP1(0x30000000), VP1(0x40000000)
+    waves, tpu, tot = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+
+    def call(w, s, x, y, n_sets=1, n=4096, k=4096, launches=2, stamps=0x50000000,
+             words=1 << 40):
+        return lib.cq_int4_timeline(b"int4gemv_cdna4", w, s, x, y, n_sets, n, k, None,
+                                    0, 0.0, 0.0, launches, stamps, words,
+                                    ctypes.byref(waves), ctypes.byref(tpu),
+                                    ctypes.byref(tot))
+
+    assert call(w, s, x, y, stamps=None) == _capi.CQ_ERR_INVALID_ARG
+    assert "null" in _capi.last_error()
+    assert call(None, s, x, y) == _capi.CQ_ERR_INVALID_ARG
+    assert call(w, s, x, y, launches=0) == _capi.CQ_ERR_INVALID_ARG
+    assert "n_launches" in _capi.last_error()
+    assert call(VP1(0x10000001), s, x, y) == _capi.CQ_ERR_INVALID_ARG
+    assert "covers the LDS kernel" in _capi.last_error()
+    # 4096 x 4096: 512 workgroups of 512 threads, 4096 waves, 8 words each
+    assert call(w, s, x, y, launches=3, words=3 * 4096 * 8 - 1) == _capi.CQ_ERR_INVALID_ARG
+    assert "stamps holds" in _capi.last_error()
+    two = ctypes.c_void_p * 2
+    w2 = two(0x10000000, 0x11000000)
+    s2 = two(0x20000000, 0x21000000)
+    y2 = two(0x40000000, 0x41000000)
+    x2 = two(0x30000000, 0x31000008)    # the second x is off 16-byte alignment
+    assert call(w2, s2, x2, y2, n_sets=2) == _capi.CQ_ERR_INVALID_ARG
+    assert "set 1" in _capi.last_error()
+
+
 def _prepare(lib, op, variant, w, s, x, y, n, k):
     rec = _capi.CqPrepared()
     for i in range(12):

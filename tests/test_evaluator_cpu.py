@@ -449,3 +449,28 @@ def test_negative_runner_records_and_pass_rule():
                     "n_pass_expected": 1, "n_pass_ok": 1, "n_skipped": 1,
                     "n_passed": 2, "all_pass": False}
     assert N.summarize_cases(recs[:1] + recs[2:])["all_pass"]
+
+
+def test_timeline_summary_of_known_stamps():
+    """The timeline's reduction on hand-made stamps (100 ticks per us):
+    per launch, each point's median and maximum over the waves from the
+    launch's first wave start; the span to its last y store; the gap to the
+    next launch's first start; medians over the launches kept."""
+    import numpy as np
+    from cudalab_amd.evaluator.timeline import POINTS, summarize
+    base = np.array([[0, 100, 150, 160, 170],      # wave 0 (ticks)
+                     [20, 110, 200, 230, 250],     # wave 1
+                     [40, 120, 210, 240, 260]])    # wave 2
+    L = 3
+    a = np.zeros((L, 3, 8), dtype=np.int64)
+    for i in range(L):
+        a[i, :, :5] = base + 1000 + i * 400        # launches 400 ticks apart
+    s = summarize(a, 100.0, skip=0.0)
+    assert s["launches_used"] == 2                 # the last launch has no successor
+    p = s["points"]
+    assert p[POINTS[0]] == {"p50_us": 0.2, "max_us": 0.4}
+    assert p[POINTS[1]] == {"p50_us": 1.1, "max_us": 1.2}
+    assert p[POINTS[2]] == {"p50_us": 2.0, "max_us": 2.1}
+    assert p[POINTS[4]] == {"p50_us": 2.5, "max_us": 2.6}
+    assert s["span_us"] == pytest.approx(2.6)
+    assert s["gap_us"] == pytest.approx(4.0 - 2.6)

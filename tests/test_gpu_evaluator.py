@@ -100,3 +100,37 @@ def test_api_cost_paths_all_launch(cuda):
     for name, rec in res["host_us_per_call"].items():
         assert rec["us"] is not None and rec["samples"] == 2, name
         assert rec["us"] > 0.5 * floor, (name, rec, floor)
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (11008, 4096), (4096, 11008), (300, 1280)])
+def test_timeline_stamps_every_wave_and_keeps_the_outputs(ext4, N, K):
+    """cq_int4_timeline runs a stamped copy of the LDS kernel: every wave of
+    every timed launch leaves five stamps in order (start <= x barrier <=
+    first chunk <= last chunk <= y stored), the launches follow one another,
+    and each set's y is bit-identical to forward_into's (the copy keeps the
+    product kernel's arithmetic).  Plans covered: one row per lane on 512
+    threads, two rows per lane on 256, six chunks per lane, a short row."""
+    import numpy as np
+    import torch
+    from cudalab_amd.evaluator.timeline import run_stamped, summarize
+    from cudalab_amd.operators.int4gemv import device_random_set
+    sets = [device_random_set(N, K, 900 + i) for i in range(3)]
+    announce(f"timeline {N}x{K}")
+    r = run_stamped("int4gemv_cdna4", sets, n_launches=6, warmup=3, burn_ms=0.0,
+                    delay_us=2000.0)
+    a = r["stamps"]
+    d = ext4.describe("int4gemv_cdna4", sets[0][0], sets[0][2])
+    assert a.shape == (6, int(d["grid"]) * int(d["block"]) // 64, 8)
+    t = a[:, :, :5]
+    assert (t > 0).all()
+    assert (np.diff(t, axis=2) >= 0).all()
+    starts = t[:, :, 0].min(axis=1)
+    ends = t[:, :, 4].max(axis=1)
+    assert (starts[1:] >= ends[:-1] - 5).all()    # one stream: launches in order (50 ns slack)
+    s = summarize(a, r["ticks_per_us"], skip=0.0)
+    assert s["launches_used"] == 5 and 0 < s["span_us"] < 1000
+    for W, sc, x, out in sets:
+        want = torch.empty_like(out)
+        ext4.forward_into("int4gemv_cdna4", W, sc, x, want)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
