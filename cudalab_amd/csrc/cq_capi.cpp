@@ -734,6 +734,17 @@ int cq_int4_timeline(const char* variant, const void* const* w,
                     "stamps holds " + std::to_string(stamps_words) + " words; " +
                         std::to_string(n_launches) + " launches of " +
                         std::to_string(waves) + " waves need 8 per wave");
+    // the kernel writes the stamps while it reads the sets: no shared byte
+    Span sp;
+    sp.lo = reinterpret_cast<uintptr_t>(stamps);
+    sp.hi = sp.lo + static_cast<unsigned __int128>(n_launches * waves * 8) * 8;
+    for (int64_t i = 0; i < n_sets; ++i) {
+        const Operands o = operand_spans(CQ_OP_INT4GEMV, w[i], scale[i], x[i], y[i], n, k);
+        if (overlaps(sp, o.w) || overlaps(sp, o.scale) || overlaps(sp, o.x) ||
+            overlaps(sp, o.y))
+            return fail(CQ_ERR_INVALID_ARG,
+                        "stamps overlap an operand of set " + std::to_string(i));
+    }
     int dev = 0, khz = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");

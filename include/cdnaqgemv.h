@@ -295,7 +295,8 @@ int cq_launch_floor(int64_t grid, int block, void* sink, void* stream,
  * stamps.  `stamps` is device memory of `stamps_words` (at least
  * n_launches * waves * 8) 64-bit words.  *ticks_per_us is the clock's rate,
  * *total_us the window's event time.  CQ_ERR_INVALID_ARG when a set's plan
- * is not the LDS kernel (the scalar or K-tiled kernels are not covered).
+ * is not the LDS kernel (the scalar or K-tiled kernels are not covered) or
+ * when the stamps share a byte with an operand of a set.
  */
 int cq_int4_timeline(const char* variant, const void* const* w,
                      const void* const* scale, const void* const* x,

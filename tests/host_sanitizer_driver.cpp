@@ -56,6 +56,27 @@ int main() {
     cq_read_ceiling(bufs, 2, 4096, Y, nullptr, 0, 0.0, 0.0, 1, &tot);
     cq_launch_floor(0, 256, Y, nullptr, 0, 0.0, 0.0, 1, &tot);
     cq_launch_floor(256, 256, Y, nullptr, 0, 0.0, 1e7, 1, &tot);
+    // timeline: refused before any launch (null, non-LDS plan, small or
+    // overlapping stamp buffer)
+    {
+        const void* tw[1] = {(const void*)0x10000000};
+        const void* ts[1] = {(const void*)0x20000000};
+        const void* tx[1] = {(const void*)0x30000000};
+        void* ty[1] = {(void*)0x40000000};
+        const void* tw_bad[1] = {(const void*)0x10000001};
+        int64_t waves = 0; double tpu = 0;
+        cq_int4_timeline("int4gemv_cdna4", tw, ts, tx, ty, 1, 4096, 4096, nullptr, 0, 0.0, 0.0, 2,
+                         nullptr, 1 << 20, &waves, &tpu, &tot);
+        cq_int4_timeline("int4gemv_cdna4", tw_bad, ts, tx, ty, 1, 4096, 4096, nullptr, 0, 0.0, 0.0, 2,
+                         (uint64_t*)0x50000000, 1 << 20, &waves, &tpu, &tot);
+        cq_int4_timeline("int4gemv_cdna4", tw, ts, tx, ty, 1, 4096, 4096, nullptr, 0, 0.0, 0.0, 2,
+                         (uint64_t*)0x50000000, 7, &waves, &tpu, &tot);
+        cq_int4_timeline("int4gemv_cdna4", tw, ts, tx, ty, 1, 4096, 4096, nullptr, 0, 0.0, 0.0, 2,
+                         (uint64_t*)0x107FFFF8, int64_t(1) << 40, &waves, &tpu, &tot);
+        cq_int4_timeline("int4gemv_cdna4", tw, ts, tx, ty, 1, 4096, 4096, nullptr, 0, 0.0, 0.0,
+                         INT64_MAX, (uint64_t*)0x50000000, INT64_MAX, &waves, &tpu, &tot);
+        std::printf("timeline: %s\n", cq_last_error());
+    }
     // describe, every op and size class
     for (int op : {CQ_OP_INT4GEMV, CQ_OP_QGEMV, CQ_OP_GEMV_F16, CQ_OP_GEMV_F32})
         for (int64_t n : {1, 7, 4096, 8192, 1 << 20})

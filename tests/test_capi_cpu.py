@@ -285,7 +285,7 @@ def test_timeline_refuses_before_any_launch():
     """cq_int4_timeline's refusals come from host checks alone (fake,
     disjoint device addresses; nothing is launched): null arguments, a set
     whose plan is not the LDS kernel (a misaligned W takes the scalar
-    kernel), a stamp buffer too small."""
+    kernel), a stamp buffer too small or overlapping an operand."""
     lib = _capi.load()
     VP1 = ctypes.c_void_p * 1
     w, s, x, y = VP1(0x10000000), VP1(0x20000000), VP1(0x30000000), VP1(0x40000000)
@@ -308,6 +308,9 @@ def test_timeline_refuses_before_any_launch():
     # 4096 x 4096: 512 workgroups of 512 threads, 4096 waves, 8 words each
     assert call(w, s, x, y, launches=3, words=3 * 4096 * 8 - 1) == _capi.CQ_ERR_INVALID_ARG
     assert "stamps holds" in _capi.last_error()
+    # stamps that share a byte with a set's operand (here: the end of W)
+    assert call(w, s, x, y, stamps=0x10000000 + 4096 * 2048 - 8) == _capi.CQ_ERR_INVALID_ARG
+    assert "overlap an operand of set 0" in _capi.last_error()
     two = ctypes.c_void_p * 2
     w2 = two(0x10000000, 0x11000000)
     s2 = two(0x20000000, 0x21000000)
