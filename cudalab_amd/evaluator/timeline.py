@@ -141,11 +141,13 @@ def main(argv=None) -> int:
     ap.add_argument("--launches", type=int, default=400)
     ap.add_argument("--json", default=None)
     args = ap.parse_args(argv)
-    if args.launches < 2:
-        ap.error("--launches must be >= 2")
+    if args.launches < 2 or args.n < 1 or args.k < 128 or args.k % 128:
+        print("timeline: --launches >= 2, --n >= 1 and --k a positive multiple of 128",
+              file=sys.stderr)
+        return 2
     if not torch.cuda.is_available():
         print("timeline: no GPU visible", file=sys.stderr)
-        return 2
+        return 1
     rec = run(args.n, args.k, args.variant, args.launches)
     print(table(rec), flush=True)
     if args.json:

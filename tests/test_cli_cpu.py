@@ -158,3 +158,16 @@ def test_decode_stress_option(monkeypatch, capsys):
     assert decode.main(["--stress", "--op", "qgemv"]) == 1
     assert "no GPU visible" in capsys.readouterr().err
     assert decode.STRESS_SHAPES == ((11008, 4096), (4096, 11008)) + ((4096, 4096),) * 4
+
+
+def test_timeline_options(monkeypatch, capsys):
+    """The timeline command rejects impossible sizes before touching a GPU
+    and needs one to run."""
+    import torch
+    from cudalab_amd.evaluator import timeline
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert timeline.main(["--n", "4096", "--k", "11008"]) == 1
+    for bad in (["--launches", "1"], ["--k", "100"], ["--n", "0"]):
+        assert timeline.main(bad) == 2, bad
+    err = capsys.readouterr().err
+    assert "no GPU visible" in err and "multiple of 128" in err
