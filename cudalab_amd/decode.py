@@ -33,7 +33,7 @@ Usage: python -m cudalab_amd.decode [--model 7b|70b] [--layers N]
        [--modes sequential,grouped,graph]
        python -m cudalab_amd.decode --stress [--op int4gemv|qgemv] [--steps 20]
 
---stress times the decode stress sequence of the measurement plan instead:
+--stress times the decode stress sequence instead, Llama-7B projection shapes
 (N, K) = (11008, 4096), (4096, 11008), then four (4096, 4096), back to back,
 over an HBM-cold pool of distinct weights, replayed from a HIP graph and
 run eager.
@@ -205,8 +205,8 @@ def time_steps(fn, steps: int, warmup: int) -> float:
 
 MODES = ("sequential", "grouped", "graph")
 
-# The decode stress sequence of the measurement plan: the 7B MLP pair, then
-# four 4096^2 projections, back to back (each launch's input is its own x).
+# The decode stress sequence: Llama-7B projection shapes back to back, the
+# MLP pair and then four 4096^2 projections (each launch's input is its own x).
 STRESS_SHAPES = ((11008, 4096), (4096, 11008), (4096, 4096), (4096, 4096),
                  (4096, 4096), (4096, 4096))
 STRESS_POOL_BYTES = 512 << 20

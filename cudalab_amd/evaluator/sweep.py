@@ -66,8 +66,8 @@ def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
     distinct sets for "streaming" and "misaligned", one set for "hot".
     INT4/INT8 sets are (W, scale, x, out); FP16 sets are (W, x, out).
     "misaligned" moves W one byte (INT4/INT8; two for FP16) and x two bytes
-    off their 16-byte alignment, the measurement plan's misaligned case:
-    every call then runs the scalar kernel, as the reference's did."""
+    off their 16-byte alignment (the offsets of the reference's fallback
+    tests): every call then runs the scalar kernel, as the reference's did."""
     if op == "int4gemv":
         from ..operators.int4gemv import device_random_set
     elif op == "gemv":

@@ -150,8 +150,8 @@ def test_sweep_misaligned_sets_keep_values_off_alignment():
 
 
 def test_decode_stress_option(monkeypatch, capsys):
-    """--stress is parsed and needs a GPU; the sequence is the measurement
-    plan's: the 7B MLP pair, then four 4096^2 projections."""
+    """--stress is parsed and needs a GPU; the sequence is the 7B MLP pair,
+    then four 4096^2 projections."""
     import torch
     from cudalab_amd import decode
     monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
