@@ -479,6 +479,23 @@ def main(argv=None) -> int:
                                        "(cq_int4gemv_grouped) over distinct HBM-cold "
                                        "sets, from a HIP graph: the per-launch cost "
                                        "shared by 8 GEMVs; not the headline caliber")
+        if plan.get("kernel") == "lds":
+            from cudalab_amd.evaluator.timeline import run_stamped, summarize
+            tl = run_stamped(args.variant, sets, n_launches=400, warmup=args.warmup,
+                             burn_ms=100.0)
+            ts = summarize(tl["stamps"], tl["ticks_per_us"])
+            detail["wave_timeline"] = {
+                "span_us": round(ts["span_us"], 3),
+                "gap_us": round(ts["gap_us"], 3),
+                "points_us": {p: [round(v["p50_us"], 3), round(v["max_us"], 3)]
+                              for p, v in ts["points"].items()},
+                "instrumented_us_per_call": round(tl["us_per_launch"], 4),
+                "note": "cq_int4_timeline over the same pool: a stamped copy of this "
+                        "plan's kernel (same arithmetic and launch shape), 400 "
+                        "launches; per point [median wave, last wave] in us from "
+                        "each launch's first wave start; span = first wave start "
+                        "to last y store, gap = last y store to the next launch's "
+                        "first wave start (medians over launches)"}
         gpu_loop("int4gemv", args.variant, sets[:1], nl, args.warmup, 100.0)
         h = windows("int4gemv", args.variant, sets[:1], nl)
         detail["hot_us_per_call"] = round(h["median"], 4)
