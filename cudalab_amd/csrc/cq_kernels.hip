@@ -397,6 +397,13 @@ __device__ __forceinline__ uint64_t wall_clock_through(float& v) {
     asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t), "+v"(v));
     return t;
 }
+__device__ __forceinline__ uint64_t wall_clock_through(uint32_t& a, uint32_t& b,
+                                                       uint32_t& c) {
+    uint64_t t;
+    asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(t), "+v"(a), "+v"(b), "+v"(c));
+    return t;
+}
 
 // The rows of logical workgroup `blk` of one INT4 problem.  `xs` is the
 // workgroup's LDS: [4][CW*J + 1] re-paired x pieces, q-major.
@@ -480,14 +487,23 @@ __device__ __forceinline__ void int4_lds_rows(
     if (tid < 4) xs[tid * S + CW * J] = uint4{0, 0, 0, 0};
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (STAMP) ts[1] = wall_clock64();
+    // nibble masks and byte shift of the dequant; the stamped copy passes
+    // them through the barrier stamp's clock read, so no dequant (nor its
+    // wait for the weights) is placed above that read
+    uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, sh8 = 8;
+    if constexpr (STAMP) ts[1] = wall_clock_through(m_lo, m_hi, sh8);
     uint4 xp[J][4];
     const int xlast = clast < nchunks ? clast : CW * J;
+    // the stamped copy reads each chunk's x next to its use (below): its
+    // clock reads keep loads from crossing them, and reads issued all up
+    // front would hold J x 16 VGPRs at once
+    if constexpr (!STAMP) {
 #pragma unroll
-    for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            xp[j][q] = xs[q * S + (j < J - 1 ? col + CW * j : xlast)];
+            for (int q = 0; q < 4; ++q)
+                xp[j][q] = xs[q * S + (j < J - 1 ? col + CW * j : xlast)];
+    }
 
     const f16x2 bias_lo = {static_cast<_Float16>(-1032.0f),
                            static_cast<_Float16>(-1032.0f)};
@@ -498,21 +514,30 @@ __device__ __forceinline__ void int4_lds_rows(
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z,
-                                       wv[r][j].w};
+            if constexpr (STAMP) {
+                if (r == 0) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        xp[j][q] = xs[q * S + (j < J - 1 ? col + CW * j : xlast)];
+                }
+            }
             float d = 0.f;
             if constexpr (STAMP) {
-                // the second chunk's sum starts after the first stamp
-                if (r * J + j == 1) asm volatile("" : "+v"(d) : "v"(acc));
+                // the second chunk's dequant and sum start after the first stamp
+                if (r * J + j == 1)
+                    asm volatile("" : "+v"(d), "+v"(wv[r][j].x), "+v"(wv[r][j].y),
+                                 "+v"(wv[r][j].z), "+v"(wv[r][j].w) : "v"(acc));
             }
+            const uint32_t words[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z,
+                                       wv[r][j].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const uint32_t u = words[q];
-                const uint32_t u8 = u >> 8;
-                const f16x2 qa = as_f16x2((u & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
-                const f16x2 qb = as_f16x2((u & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
-                const f16x2 qc = as_f16x2((u8 & 0x000F000Fu) ^ 0x64086408u) + bias_lo;
-                const f16x2 qd = as_f16x2((u8 & 0x00F000F0u) ^ 0x54805480u) + bias_hi;
+                const uint32_t u8 = u >> sh8;
+                const f16x2 qa = as_f16x2((u & m_lo) ^ 0x64086408u) + bias_lo;
+                const f16x2 qb = as_f16x2((u & m_hi) ^ 0x54805480u) + bias_hi;
+                const f16x2 qc = as_f16x2((u8 & m_lo) ^ 0x64086408u) + bias_lo;
+                const f16x2 qd = as_f16x2((u8 & m_hi) ^ 0x54805480u) + bias_hi;
                 d = __builtin_amdgcn_fdot2(qa, as_f16x2(xp[j][q].x), d, false);
                 d = __builtin_amdgcn_fdot2(qb, as_f16x2(xp[j][q].y), d, false);
                 d = __builtin_amdgcn_fdot2(qc, as_f16x2(xp[j][q].z), d, false);
