@@ -370,6 +370,72 @@ def test_ulp32_matches_spacing():
     assert np.array_equal(orc.ulp32(v), np.spacing(np.abs(v)).astype(np.float64))
 
 
+def _spacing16(v: np.ndarray) -> np.ndarray:
+    """fp16 grid spacing from numpy's own nextafter on the fp16 type: the
+    gap from |v| rounded to fp16 to the next fp16 above it, and for the
+    largest finite value (whose next value would overflow) the gap below
+    it, 65504 - 65472 = 32."""
+    a = np.abs(np.asarray(v, dtype=np.float64).astype(np.float16))
+    up = np.nextafter(a, np.float16(np.inf))
+    gap = up.astype(np.float64) - a.astype(np.float64)
+    top = a == np.float16(65504.0)
+    below = np.nextafter(a, np.float16(0.0)).astype(np.float64)
+    return np.where(top, a.astype(np.float64) - below, gap)
+
+
+def test_ulp16_matches_spacing_on_all_fp16_values():
+    """ulp16 (oracle restatement of cudalab/int4gemv_correctness.py:128-141)
+    against an independent definition over all 65536 fp16 bit patterns:
+    every finite value below 65504 gets np.spacing's fp16 gap, 65504 gets
+    32, subnormals and zeros get 2^-24."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = bits.view(np.float16)
+    fin = np.isfinite(v)
+    vf = v[fin]
+    got = orc.ulp16(vf.astype(np.float64))
+    want = _spacing16(vf)
+    assert np.array_equal(got, want)
+    a = np.abs(vf.astype(np.float64))
+    below_max = a < 65504.0
+    assert np.array_equal(got[below_max],
+                          np.spacing(np.abs(vf[below_max])).astype(np.float64))
+    assert np.all(got[a == 65504.0] == 32.0)
+    sub = a < 2.0 ** -14
+    assert sub.sum() == 2 * 1024          # +-0 and the 1023 subnormals each side
+    assert np.all(got[sub] == 2.0 ** -24)
+    assert fin.sum() == 63488             # 65536 - 2 infinities - 2046 NaNs
+
+
+def test_ulp16_rounds_to_fp16_before_measuring():
+    # values that round into the next binade take that binade's spacing
+    v = np.array([1.0 + 2.0 ** -12, 2.0 - 2.0 ** -13, 65519.0, 3e-8, -0.0])
+    got = orc.ulp16(v)
+    assert np.array_equal(got, _spacing16(v))
+    assert list(got) == [2.0 ** -10, 2.0 ** -9, 32.0, 2.0 ** -24, 2.0 ** -24]
+
+
+def test_ulp16_pin_rejects_planted_mistakes():
+    """Plausible slips in the ulp formula fail the pin above (planted here on
+    the CPU, in copies of the formula): a factor of two either way, ceil for
+    floor, and the subnormal floor taken as 2^-14."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = bits.view(np.float16)
+    vf = v[np.isfinite(v)]
+    want = _spacing16(vf)
+    a = np.abs(vf.astype(np.float64))
+    tiny = 2.0 ** -14
+    with np.errstate(divide="ignore"):
+        lg = np.log2(np.maximum(a, tiny))
+    mistakes = {
+        "half": np.where(a >= tiny, 2.0 ** (np.floor(lg) - 11), 2.0 ** -24),
+        "double": np.where(a >= tiny, 2.0 ** (np.floor(lg) - 9), 2.0 ** -24),
+        "ceil": np.where(a >= tiny, 2.0 ** (np.ceil(lg) - 10), 2.0 ** -24),
+        "sub_floor": np.where(a >= tiny, 2.0 ** (np.floor(lg) - 10), tiny),
+    }
+    for name, bad in mistakes.items():
+        assert not np.array_equal(bad, want), name
+
+
 @pytest.mark.parametrize("dt", [np.float16, np.float32])
 def test_gemv_gate_accepts_cpu_gemv_and_rejects_planted_mistakes(dt):
     rng = np.random.default_rng(11)
