@@ -15,7 +15,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-from .build import FAST_NAME, LIB_PATH, fast_module_path, source_hash
+from .build import FAST_NAME, LIB_PATH, fast_abi_stamp, fast_module_path, source_hash
 
 CQ_OK = 0
 CQ_ERR_UNKNOWN_VARIANT = 1
@@ -186,7 +186,8 @@ _fast = None
 def fast_module():
     """The eager fast-path module (`_cqfast`, built beside the library from
     csrc/cq_pyfast.cpp), loaded once; refused, like the library, when
-    missing or built from other sources than the tree holds."""
+    missing, built from other sources than the tree holds, or built against
+    another torch (version, C++ ABI flag or g++ flags: `fast_abi_stamp`)."""
     global _fast
     if _fast is not None:
         return _fast
@@ -208,6 +209,12 @@ def fast_module():
                 f"{path} was built from other sources than the tree holds "
                 f"(module src={mod.src_hash}, tree src={source_hash()}); rebuild "
                 "it with `python -m cudalab_amd.build`.")
+        abi = getattr(mod, "abi_stamp", "unstamped")
+        if abi != fast_abi_stamp():
+            raise StaleLibrary(
+                f"{path} was built against another torch or with other flags "
+                f"(module {abi}, this process {fast_abi_stamp()}); rebuild it "
+                "with `python -m cudalab_amd.build`.")
         _fast = mod
         return mod
 

@@ -109,6 +109,24 @@ def fast_module_path() -> Path:
     return LIB_DIR / (FAST_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
 
+_FAST_FLAGS = ("-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+               "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1")
+_FAST_LIBS = ("-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python")
+
+
+def fast_abi_stamp() -> str:
+    """What the fast-path module's binary interface depends on besides its
+    sources: the torch version it was compiled against, torch's C++ ABI
+    flag, and the compile flags and libraries of its g++ line (the include
+    and library directories are left out: they name this machine's paths).
+    Compiled into the module and compared on load, so a module built
+    against another torch is refused rather than imported."""
+    import torch
+    h = hashlib.sha256(" ".join(_FAST_FLAGS + _FAST_LIBS).encode()).hexdigest()[:12]
+    return (f"torch={torch.__version__};"
+            f"cxx11abi={int(torch._C._GLIBCXX_USE_CXX11_ABI)};flags={h}")
+
+
 def _fast_module_cmd(out: Path, stamp: str) -> list[str]:
     """g++ line of the fast-path module: torch's and Python's headers, HIP's
     host headers (for the current-stream query), linked against torch's
@@ -120,17 +138,19 @@ def _fast_module_cmd(out: Path, stamp: str) -> list[str]:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     incs = [*include_paths(), sysconfig.get_paths()["include"],
             str(Path(rocm) / "include"), str(INCLUDE)]
-    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
-            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+    return ["g++", *_FAST_FLAGS,
             f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
-            stamp, *[f"-I{p}" for p in incs], str(CSRC / FAST_SOURCE),
-            "-o", str(out), *[f"-L{p}" for p in library_paths()],
-            "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python"]
+            stamp, f"-DCQ_FAST_ABI=\"{fast_abi_stamp()}\"",
+            *[f"-I{p}" for p in incs], str(CSRC / FAST_SOURCE),
+            "-o", str(out), *[f"-L{p}" for p in library_paths()], *_FAST_LIBS]
 
 
 def build_library(verbose: bool = False) -> Path:
     """Compile `libcdnaqgemv.so` and the fast-path module in-tree (always
-    compiles; atomic replace)."""
+    compiles; atomic replace).  The library is required; the fast-path
+    module is best effort: if its g++ step fails the library is still
+    installed, any earlier module is removed, and the operators take the
+    checked path for every call (ext.py warns once)."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="cq_build_", dir=LIB_DIR) as tmp:
@@ -143,11 +163,17 @@ def build_library(verbose: bool = False) -> Path:
             cmds.append([cc, *HIPCC_FLAGS, stamp, f"-I{INCLUDE}", f"-I{CSRC}",
                          "-c", str(CSRC / src), "-o", str(obj)])
         fast_tmp = Path(tmp) / fast_module_path().name
-        cmds.append(_fast_module_cmd(fast_tmp, stamp))
-        with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        with ThreadPoolExecutor(max_workers=len(cmds) + 1) as ex:
+            fast_job = ex.submit(_run, _fast_module_cmd(fast_tmp, stamp))
             for f in [ex.submit(_run, c) for c in cmds]:
                 f.result()
-        os.replace(fast_tmp, fast_module_path())
+            try:
+                fast_job.result()
+                os.replace(fast_tmp, fast_module_path())
+            except (RuntimeError, OSError) as e:
+                fast_module_path().unlink(missing_ok=True)
+                print(f"warning: the eager fast-path module was not built; "
+                      f"every call takes the checked path ({e})", file=sys.stderr)
         out_tmp = Path(tmp) / LIB_NAME
         _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs,
               "-o", str(out_tmp)])

@@ -837,6 +837,7 @@ int cq_prepare(int op, const char* variant, const void* w, const void* scale,
 }
 
 int cq_launch_prepared(const cq_prepared_t* prepared, void* stream) {
+    g_last_error.clear();
     if (prepared == nullptr) return fail(CQ_ERR_INVALID_ARG, "prepared record pointer is NULL");
     Prepared rec;
     std::memcpy(&rec, prepared, sizeof rec);

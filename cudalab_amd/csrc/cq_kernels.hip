@@ -1280,13 +1280,19 @@ struct Int4Wave {
         else return nullptr;
     }
 };
+// The INT4 plans take 512-thread workgroups only with one row per lane
+// (lds_threads), so only those instances exist at 512 threads.
+template <int NT, int R>
+constexpr bool int4_lds_shape(int j) {
+    return R <= int4_rmax(j) && (NT != 512 || R == 1);
+}
 template <int NT>
 struct Int4Lds {
     using Fn = Int4Fn;
     static constexpr int kMaxJ = kInt4MaxJ;
     template <int CW, int J, int R>
     static constexpr Fn get() {
-        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_kernel<CW, J, R, NT>;
+        if constexpr (int4_lds_shape<NT, R>(J)) return &int4gemv_lds_kernel<CW, J, R, NT>;
         else return nullptr;
     }
 };
@@ -1318,7 +1324,7 @@ struct Int4LdsStamp {
     static constexpr int kMaxJ = kInt4MaxJ;
     template <int CW, int J, int R>
     static constexpr Fn get() {
-        if constexpr (R <= int4_rmax(J)) return &int4gemv_lds_stamp_kernel<CW, J, R, NT>;
+        if constexpr (int4_lds_shape<NT, R>(J)) return &int4gemv_lds_stamp_kernel<CW, J, R, NT>;
         else return nullptr;
     }
 };
@@ -1651,6 +1657,7 @@ hipError_t launch_int4_stamped(const Plan& p, const void* w, const void* scale,
                                const void* x, void* y, int64_t n, int64_t k,
                                uint64_t* stamps, hipStream_t stream) {
     if (p.kind != kLds || !lds_chunks_ok(p, k / 32)) return hipErrorInvalidConfiguration;
+    if (p.block != 512 && p.block != kBlock) return hipErrorInvalidConfiguration;
     const Int4StampFn fn = p.block == 512 ? instance<Int4LdsStamp<512>>(p.cw, p.j, p.r)
                                           : instance<Int4LdsStamp<kBlock>>(p.cw, p.j, p.r);
     if (fn == nullptr) return hipErrorInvalidConfiguration;

@@ -42,6 +42,9 @@
 
 namespace py = pybind11;
 
+#ifndef CQ_FAST_ABI
+#define CQ_FAST_ABI "unstamped"
+#endif
 #ifndef CQ_SRC_HASH
 #define CQ_SRC_HASH "unstamped"
 #endif
@@ -341,6 +344,7 @@ private:
 PYBIND11_MODULE(_cqfast, m) {
     m.doc() = "Checked-once launch path of the eager GEMV API (see ext.py)";
     m.attr("src_hash") = CQ_SRC_HASH;
+    m.attr("abi_stamp") = CQ_FAST_ABI;   // torch version, C++ ABI, g++ flags
     py::class_<Launcher>(m, "Launcher")
         .def(py::init<int, const std::vector<std::string>&, uintptr_t, uintptr_t,
                       uintptr_t, int64_t, uintptr_t>(),

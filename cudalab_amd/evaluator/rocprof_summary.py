@@ -6,7 +6,7 @@ Three reports, all printed to stdout:
            (count, mean, median, min, max, and the median gap between
            consecutive dispatches of the same kernel); optionally the
            matched kernel's figures as JSON for bench.py's
-           `rocprof_us_per_dispatch` field
+           `rocprof_isolated_dispatch_us` field
   counters per-dispatch medians of every counter in one or more `--pmc`
            runs, for the kernels matching each --match string
   traffic  HBM bytes per dispatch of one kernel from two `--pmc` runs

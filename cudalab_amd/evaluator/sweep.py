@@ -92,10 +92,17 @@ def make_sets(op: str, N: int, K: int, mode: str, seed: int = 1234):
 
 
 def window_us(op: str, variant: str, sets, steps: int, warmup: int) -> float:
+    """µs per call of one pre-filled window; a window whose enqueue
+    outlasted its on-device wait is timed again behind a wait twice the
+    enqueue time."""
     torch.cuda.synchronize()
     r = pool_timing(op, variant, sets, warmup=warmup, n_launches=steps,
                     per_kernel=False, burn_ms=100.0,
                     delay_us=prefill_delay_us(steps))
+    if not r["prefilled"]:
+        r = pool_timing(op, variant, sets, warmup=0, n_launches=steps,
+                        per_kernel=False,
+                        delay_us=min(1e6, 2.0 * r["host_us"] + 500.0))
     torch.cuda.synchronize()
     return r["total_us"] / steps
 

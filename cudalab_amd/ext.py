@@ -29,6 +29,7 @@ depending on the host).
 from __future__ import annotations
 
 import ctypes
+import warnings
 from typing import Optional
 
 import torch
@@ -63,9 +64,46 @@ _FAST_KIND = {"int4gemv": 0, "qgemv": 1, "gemv": 2}
 _GROUPED_ENTRY = {"int4gemv": "cq_int4gemv_grouped", "qgemv": "cq_qgemv_grouped"}
 
 
+class _DeclineAll:
+    """Stand-in for the fast-path launcher when its module is missing, stale
+    or fails to import: it accepts no call, so every call takes the checked
+    path (which launches the same HIP kernels through the library)."""
+
+    def accepts(self, *args) -> bool:
+        return False
+
+    gemv_accepts = knows = into = gemv_into = grouped = accepts
+
+    def forward(self, *args):
+        return None
+
+    gemv_forward = forward
+
+    def cached(self) -> int:
+        return 0
+
+    def clear(self) -> None:
+        pass
+
+
+_fast_warned = False
+
+
 def _fast_launcher(op: str, names: list[str]):
+    """The fast-path launcher of `op`, or a launcher that declines every
+    call (with one warning per process) when the fast-path module cannot
+    be used; the checked path is complete without it."""
+    global _fast_warned
     grouped = _GROUPED_ENTRY.get(op)
-    return _capi.fast_module().Launcher(
+    try:
+        mod = _capi.fast_module()
+    except (_capi.LibraryMissing, _capi.StaleLibrary, ImportError, OSError) as e:
+        if not _fast_warned:
+            _fast_warned = True
+            warnings.warn(f"eager fast path unavailable, every call takes the "
+                          f"checked path: {e}", RuntimeWarning, stacklevel=3)
+        return _DeclineAll()
+    return mod.Launcher(
         _FAST_KIND[op], names, _capi.entry_address("cq_prepare"),
         _capi.entry_address("cq_launch_prepared"),
         _capi.entry_address("cq_last_error"), FAST_CACHE_ENTRIES,
@@ -625,7 +663,9 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
     passed; `delay_us` > 0 queues an on-device wait before the start event
     so the host enqueues the window ahead of the GPU (see
     prefill_delay_us).  Returns {"total_us": window event time,
-    "host_us": host time spent enqueuing the window, "kernel_us":
+    "host_us": host time spent enqueuing the window, "prefilled": whether
+    a wait was queued and outlasted that enqueue (if not, the GPU may have
+    reached the window before the host finished it), "kernel_us":
     per-launch device durations (list) or None}."""
     lib = _capi.load()
     n = len(sets)
@@ -654,7 +694,10 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
             n_launches, ku, ctypes.byref(tot), ctypes.byref(host))
     if st != _capi.CQ_OK:
         _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")
+    # the wait covered the window's enqueue when the host finished enqueueing
+    # before the wait ended: the GPU then met the whole window back to back
     return {"total_us": tot.value, "host_us": host.value,
+            "prefilled": delay_us > 0 and host.value < delay_us,
             "kernel_us": [float(v) for v in ku] if ku is not None else None}
 
 

@@ -474,3 +474,17 @@ def test_timeline_summary_of_known_stamps():
     assert p[POINTS[4]] == {"p50_us": 2.5, "max_us": 2.6}
     assert s["span_us"] == pytest.approx(2.6)
     assert s["gap_us"] == pytest.approx(4.0 - 2.6)
+
+
+def test_floor_fit_recovers_a_line():
+    """floor.fit_line: least squares t = t0 + bytes / B over the sizes from
+    8 MiB up recovers the line that generated the points (and ignores the
+    small sizes, where the launch floor dominates)."""
+    from cudalab_amd.evaluator.floor import fit_line
+    rows = [{"bytes": b, "us_per_launch": 1.25 + b / 6500e3}
+            for b in (8 << 20, 16 << 20, 64 << 20, 256 << 20)]
+    rows.append({"bytes": 1 << 20, "us_per_launch": 1.8})   # below the fit range
+    fit = fit_line(rows)
+    assert fit["points"] == 4
+    assert abs(fit["t0_us"] - 1.25) < 1e-3
+    assert abs(fit["GBps"] - 6500.0) < 0.5

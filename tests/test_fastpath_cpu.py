@@ -186,3 +186,46 @@ def test_grouped_not_taken_without_launching(exts):
     assert exts["gemv"]._fast.grouped("gemv_cdna4", [prob]) is False
     with pytest.raises(RuntimeError, match="CUDA 张量"):
         exts["int4gemv"].forward_grouped("int4gemv_cdna4", iter([prob]))
+
+
+def test_module_carries_the_torch_abi_stamp():
+    from cudalab_amd.build import fast_abi_stamp
+    assert _capi.fast_module().abi_stamp == fast_abi_stamp()
+    assert f"torch={torch.__version__};" in fast_abi_stamp()
+
+
+def test_module_built_against_another_torch_is_refused(monkeypatch):
+    """A module whose ABI stamp differs from this process's torch is refused
+    on load, like a module built from other sources."""
+    monkeypatch.setattr(_capi, "_fast", None)
+    monkeypatch.setattr(_capi, "fast_abi_stamp",
+                        lambda: "torch=0.0.0;cxx11abi=0;flags=0")
+    with pytest.raises(_capi.StaleLibrary, match="another torch"):
+        _capi.fast_module()
+
+
+def test_operators_work_without_the_fast_module(monkeypatch):
+    """With the fast-path module unusable, an operator warns once and takes
+    the checked path for every call: the launcher declines everything and
+    the checked path still raises the reference's messages."""
+    from cudalab_amd import ext as ext_mod
+
+    def missing():
+        raise _capi.LibraryMissing("no _cqfast here")
+
+    monkeypatch.setattr(_capi, "fast_module", missing)
+    monkeypatch.setattr(ext_mod, "_fast_warned", False)
+    with pytest.warns(RuntimeWarning, match="checked path"):
+        e = ext_mod.Int4gemvExt()
+    assert isinstance(e._fast, ext_mod._DeclineAll)
+    W = torch.zeros(8, 128, dtype=torch.uint8)
+    s = torch.zeros(8, 2, dtype=torch.float16)
+    x = torch.zeros(256, dtype=torch.float16)
+    out = torch.zeros(8, dtype=torch.float16)
+    assert e._fast.into("int4gemv_cdna4", W, s, x, out) is False
+    assert e._fast.forward("int4gemv_cdna4", W, s, x) is None
+    assert e._fast.grouped("int4gemv_cdna4", [(W, s, x, out)]) is False
+    with pytest.raises(RuntimeError, match="CUDA 张量"):
+        e.forward_into("int4gemv_cdna4", W, s, x, out)
+    g = ext_mod.GemvExt()          # second operator: no second warning
+    assert isinstance(g._fast, ext_mod._DeclineAll)

@@ -376,7 +376,8 @@ def _spacing16(v: np.ndarray) -> np.ndarray:
     largest finite value (whose next value would overflow) the gap below
     it, 65504 - 65472 = 32."""
     a = np.abs(np.asarray(v, dtype=np.float64).astype(np.float16))
-    up = np.nextafter(a, np.float16(np.inf))
+    with np.errstate(over="ignore"):        # 65504's next value is inf
+        up = np.nextafter(a, np.float16(np.inf))
     gap = up.astype(np.float64) - a.astype(np.float64)
     top = a == np.float16(65504.0)
     below = np.nextafter(a, np.float16(0.0)).astype(np.float64)
