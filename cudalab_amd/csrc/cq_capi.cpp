@@ -803,16 +803,21 @@ int cq_describe_launch(int op, const char* variant, int64_t n, int64_t k,
     const int st = check_call(op, variant, &v, w, w, x, w, n, k);
     if (st != CQ_OK) return -st;
     const cq::Plan p = make_plan(op, *v, n, k, w, x);
+    // the launch the plan resolves to (nothing is enqueued), for its LDS bytes
+    cq::Launch L;
+    const void* sc = is_gemv(op) ? nullptr : w;
+    const long long lds = prepare_plan(op, p, w, sc, x, const_cast<void*>(w), n, k, &L) == hipSuccess
+                              ? static_cast<long long>(L.shmem) : -1;
     char line[512];
     std::snprintf(line, sizeof line,
-                  "variant=%s kernel=%s cw=%d j=%d r=%d tile=%d block=%d grid=%lld fallback=%d why=%s",
+                  "variant=%s kernel=%s cw=%d j=%d r=%d tile=%d block=%d grid=%lld lds=%lld fallback=%d why=%s",
                   v->name,
                   p.kind == cq::kScalar ? "scalar"
                   : p.kind == cq::kLds  ? "lds"
                   : p.kind == cq::kTiled ? "tiled"
                                          : "wave",
                   p.cw, p.j, p.r, p.tile,
-                  p.block, static_cast<long long>(p.grid), p.fallback ? 1 : 0,
+                  p.block, static_cast<long long>(p.grid), lds, p.fallback ? 1 : 0,
                   p.why.empty() ? "-" : p.why.c_str());
     return write_out(line, buf, cap);
 }

@@ -333,7 +333,8 @@ int cq_vec_contract_ok(int op, const void* w, const void* x, int64_t k);
  * "key=value ..." string with the keys variant, kernel (scalar, wave, lds
  * or tiled), cw (lanes per row segment), j (chunks per lane), r (rows per
  * lane), tile (chunks per lane per tile of the K-tiled kernels, else 0),
- * block, grid, fallback and, last, why (free text, "-" if none).  No
+ * block, grid, lds (dynamic LDS bytes per workgroup of that launch),
+ * fallback and, last, why (free text, "-" if none).  No
  * counterpart in the reference (its variants
  * have fixed shapes); exposed for tests and tuning records.  Returns the
  * needed length including the NUL, or a negative CQ_* status.

@@ -488,3 +488,22 @@ def test_floor_fit_recovers_a_line():
     assert fit["points"] == 4
     assert abs(fit["t0_us"] - 1.25) < 1e-3
     assert abs(fit["GBps"] - 6500.0) < 0.5
+
+
+def test_counter_report_derives_ratios():
+    """counters.derived: the ratios the occupancy/latency/stall report prints
+    come from the right counter pairs."""
+    from cudalab_amd.evaluator.counters import derived, table
+    c = {"MeanOccupancyPerCU": 4.5, "VmemLatency": 1800.0, "LdsLatency": 60.0,
+         "LdsUtil": 7.0, "TCP_TCC_READ_REQ_LATENCY": 3000.0, "TCP_TCC_READ_REQ": 3.0,
+         "SQ_WAIT_INST_LDS": 10.0, "SQ_WAIT_INST_ANY": 40.0,
+         "TA_ADDR_STALLED_BY_TC_CYCLES": 5.0, "TA_TA_BUSY": 20.0,
+         "TD_TC_STALL": 3.0, "TD_TD_BUSY": 12.0, "SQ_INSTS_VALU": 800.0,
+         "SQ_INSTS_VMEM_RD": 60.0, "SQ_WAVES": 4.0,
+         "_kernel": "void cq::(anonymous namespace)::int4gemv_lds_kernel<64, 6, 1, 512>(x)"}
+    d = derived(c)
+    assert d["l2_lat"] == 1000.0 and d["wait_lds"] == 0.25
+    assert d["ta_tc"] == 0.25 and d["td_tc"] == 0.25
+    assert d["valu_per_wave"] == 200.0 and d["vmem_per_wave"] == 15.0
+    t = table([("int4", "4096x11008", c)])
+    assert "int4gemv_lds_kernel<64, 6, 1, 512>" in t and "1800" in t
