@@ -297,6 +297,8 @@ def main(argv=None) -> int:
                     help="time the decode stress sequence (11008x4096, 4096x11008, "
                          "4 x 4096x4096) over an HBM-cold pool instead of a model")
     a = ap.parse_args(argv)
+    from . import _capi
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     if a.stress:
         if not torch.cuda.is_available():
             print("decode: no GPU visible", file=sys.stderr)

@@ -85,6 +85,8 @@ def main(argv=None) -> int:
         else:
             p.add_argument("--variants", required=True)
     a = ap.parse_args(argv)
+    from .. import _capi
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
 
     import torch
     if not torch.cuda.is_available():

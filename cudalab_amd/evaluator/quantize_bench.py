@@ -140,6 +140,7 @@ def main(argv=None) -> int:
     ap.add_argument("--launches", type=int, default=200)
     ap.add_argument("--json", default=None)
     a = ap.parse_args(argv)
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     if not torch.cuda.is_available():
         print("quantize_bench: no GPU visible", file=sys.stderr)
         return 1

@@ -264,6 +264,17 @@ def report_counters(dirs: list[Path], matches: list[str]) -> str:
     return "\n".join(lines)
 
 
+def _library_version() -> str | None:
+    """cq_version() of the tree's built library (the build the profiled run
+    loaded, when it ran from this tree); None when it cannot be loaded.
+    Loading the library makes no GPU call."""
+    try:
+        from .. import _capi
+        return _capi.version()
+    except Exception:  # noqa: BLE001
+        return None
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -291,6 +302,10 @@ def main(argv=None) -> int:
     f.add_argument("--algorithmic-bytes", type=int, default=None)
     f.add_argument("--json-out", type=Path, default=None)
     a = ap.parse_args(argv)
+    if a.cmd in ("trace", "counters"):
+        lib = _library_version()
+        if lib:
+            print(f"library: {lib}")
     if a.cmd == "trace":
         print(report_trace(a.dir, a.match, a.top, a.by_grid))
         if a.json_out:
@@ -300,6 +315,7 @@ def main(argv=None) -> int:
             print(json.dumps(rec, indent=1))
             rec["shape"] = list(a.shape) if a.shape else None
             rec["kernel_match"] = a.match
+            rec["library"] = _library_version()
             a.json_out.write_text(json.dumps(rec, indent=1) + "\n")
         return 0
     if a.cmd == "counters":
@@ -316,6 +332,7 @@ def main(argv=None) -> int:
     if a.json_out:
         rec["shape"] = list(a.shape) if a.shape else None
         rec["kernel_match"] = a.match
+        rec["library"] = _library_version()
         a.json_out.write_text(json.dumps(rec, indent=1) + "\n")
     return 0
 

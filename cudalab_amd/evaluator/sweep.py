@@ -198,6 +198,8 @@ def main(argv=None) -> int:
                          "known-size reference of counter (FETCH_SIZE / "
                          "WRITE_SIZE) runs")
     a = ap.parse_args(argv)
+    from .. import _capi
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     ops = tuple(o for o in a.ops.split(",") if o)
     if not ops or any(o not in OPS for o in ops):
         print(f"sweep: --ops must name some of {tuple(OPS)}", file=sys.stderr)

@@ -141,6 +141,7 @@ def main(argv=None) -> int:
     ap.add_argument("--launches", type=int, default=400)
     ap.add_argument("--json", default=None)
     args = ap.parse_args(argv)
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     if args.launches < 2 or args.n < 1 or args.k < 128 or args.k % 128:
         print("timeline: --launches >= 2, --n >= 1 and --k a positive multiple of 128",
               file=sys.stderr)

@@ -74,6 +74,8 @@ def main(argv=None) -> int:
     ap.add_argument("--n", type=int, default=4096)
     ap.add_argument("--k", type=int, default=4096)
     a = ap.parse_args(argv)
+    from . import _capi
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     import torch
     if not torch.cuda.is_available():
         print("gen3: no GPU visible", file=sys.stderr)

@@ -76,6 +76,8 @@ def main(argv=None) -> int:
                     default=ROOT / "experiments" / "regression" / "mi355x")
     ap.add_argument("--ops", default=",".join(OPS))
     a = ap.parse_args(argv)
+    from . import _capi
+    print(f"library: {_capi.version()}", flush=True)   # the build that ran
     ops = tuple(o for o in a.ops.split(",") if o)
     if not ops or any(o not in OPS for o in ops):
         print(f"regression: --ops must name some of {OPS}", file=sys.stderr)
