@@ -643,6 +643,20 @@ def get_ext(op: str) -> _OpExt:
     return e
 
 
+# The native loop starts its host clock after it has launched the wait and
+# recorded the start event, so the wait may already have run that long (a
+# few microseconds on MI355X hosts) when the clock starts; a window counts as
+# pre-filled only when its enqueue ended this much before the wait did.
+PREFILL_MARGIN_US = 50.0
+
+
+def window_prefilled(delay_us: float, host_us: float) -> bool:
+    """Whether a window's on-device wait outlasted the host's enqueue of the
+    window (with PREFILL_MARGIN_US to spare), so that the GPU met every
+    launch of the window already queued."""
+    return delay_us > 0 and host_us + PREFILL_MARGIN_US < delay_us
+
+
 def prefill_delay_us(n_launches: int) -> float:
     """On-device wait to queue ahead of a window of `n_launches` launches so
     that the host has enqueued all of them before the GPU reaches the first:
@@ -694,10 +708,8 @@ def pool_timing(op: str, variant: str, sets: list, warmup: int,
             n_launches, ku, ctypes.byref(tot), ctypes.byref(host))
     if st != _capi.CQ_OK:
         _fail(f"pool_timing failed (status {st}): {_capi.last_error()}")
-    # the wait covered the window's enqueue when the host finished enqueueing
-    # before the wait ended: the GPU then met the whole window back to back
     return {"total_us": tot.value, "host_us": host.value,
-            "prefilled": delay_us > 0 and host.value < delay_us,
+            "prefilled": window_prefilled(delay_us, host.value),
             "kernel_us": [float(v) for v in ku] if ku is not None else None}
 
 

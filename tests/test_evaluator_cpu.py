@@ -507,3 +507,15 @@ def test_counter_report_derives_ratios():
     assert d["valu_per_wave"] == 200.0 and d["vmem_per_wave"] == 15.0
     t = table([("int4", "4096x11008", c)])
     assert "int4gemv_lds_kernel<64, 6, 1, 512>" in t and "1800" in t
+
+
+def test_window_prefilled_needs_the_wait_to_outlast_the_enqueue_with_margin():
+    from cudalab_amd.ext import PREFILL_MARGIN_US, prefill_delay_us, window_prefilled
+    d = prefill_delay_us(2000)
+    assert window_prefilled(d, 3.0 * 2000)              # 3 us per launch: covered
+    assert not window_prefilled(d, d)                    # enqueue as long as the wait
+    assert not window_prefilled(d, d - PREFILL_MARGIN_US)  # inside the margin
+    assert window_prefilled(d, d - PREFILL_MARGIN_US - 1.0)
+    assert not window_prefilled(0.0, 0.0)                # no wait: never pre-filled
+    # the default wait leaves the margin for 20-launch windows at 8 us per launch
+    assert window_prefilled(prefill_delay_us(20), 8.0 * 20)
