@@ -11,10 +11,13 @@ start, after the x barrier, after the first and the last weight chunk are
 summed, after the y stores are issued.  Per launch, times are taken from
 the launch's first wave start; the report gives the median over launches
 of each point's median and maximum over the waves, the span (first wave
-start to last store) and the gap from a launch's last store to the next
-launch's first wave start.  The same pool is timed through the product
-kernel (cq_pool_timing) beside it: the stamps cost a little (their stores
-and clock reads), so the instrumented rate is a little slower.
+start to last store), the gap from a launch's last store to the next
+launch's first wave start, and the x barrier per workgroup: of the
+workgroup that started first on its CU and of the second, per XCD, and
+its correlation with the workgroup's start (by_workgroup).  The same pool
+is timed through the product kernel (cq_pool_timing) beside it: the stamps
+cost a little (their stores and clock reads), so the instrumented rate is a
+little slower.
 """
 from __future__ import annotations
 
@@ -104,12 +107,68 @@ def summarize(stamps: np.ndarray, ticks_per_us: float, skip: float = 0.25) -> di
             "launches_used": len(span)}
 
 
+def xcd_of_logical_block(grid: int) -> np.ndarray:
+    """XCD of each logical block under the kernels' XCD-contiguous mapping:
+    workgroup i runs on XCD i % 8 and each XCD owns one contiguous range of
+    logical blocks (cq_kernels.hip, xcd_contiguous_block)."""
+    q, r = divmod(grid, 8)
+    starts = [x * q + min(x, r) for x in range(9)]
+    out = np.empty(grid, dtype=np.int64)
+    for x in range(8):
+        out[starts[x]:starts[x + 1]] = x
+    return out
+
+
+def by_workgroup(stamps: np.ndarray, ticks_per_us: float, waves_per_group: int,
+                 skip: float = 0.25) -> dict:
+    """Per-workgroup view of the stamps (launches, waves, 8), waves in
+    logical-block order.  A workgroup's barrier time is its waves' latest
+    x-barrier stamp (they all wait at one barrier), its start their earliest
+    start, both from the launch's first wave start.  Workgroups of one launch
+    that share a hardware CU id (stamp word 5) are ranked by start: the
+    report gives the median barrier of the workgroup that started first on
+    its CU and of the second, each XCD's median, and the correlation of a
+    workgroup's start with its barrier."""
+    L, W, _ = stamps.shape
+    if W % waves_per_group:
+        raise ValueError("waves per launch not a multiple of the workgroup's waves")
+    grid = W // waves_per_group
+    lo = min(int(L * skip), max(0, L - 1))
+    t = stamps[lo:, :, :5].astype(np.float64)
+    rel = (t - t[:, :, 0].min(axis=1)[:, None, None]) / ticks_per_us
+    start = rel[:, :, 0].reshape(-1, grid, waves_per_group).min(axis=2)
+    barrier = rel[:, :, 1].reshape(-1, grid, waves_per_group).max(axis=2)
+    cu = stamps[lo:, :, 5].reshape(-1, grid, waves_per_group)[:, :, 0]
+    first, second = [], []
+    for i in range(start.shape[0]):
+        order = np.lexsort((start[i], cu[i]))
+        rank = np.zeros(grid, dtype=np.int64)
+        for a, b in zip(order[:-1], order[1:]):
+            if cu[i][b] == cu[i][a]:
+                rank[b] = rank[a] + 1
+        first.append(float(np.median(barrier[i][rank == 0])))
+        if (rank == 1).any():
+            second.append(float(np.median(barrier[i][rank == 1])))
+    xcd = xcd_of_logical_block(grid)
+    per_xcd = [float(np.median(np.median(barrier[:, xcd == x], axis=1)))
+               for x in range(8) if (xcd == x).any()]
+    return {"workgroups": grid, "launches_used": int(start.shape[0]),
+            "barrier_first_on_cu_us": statistics.median(first),
+            "barrier_second_on_cu_us": statistics.median(second) if second else None,
+            "barrier_by_xcd_us": per_xcd,
+            "corr_start_barrier": float(np.corrcoef(start.ravel(), barrier.ravel())[0, 1])}
+
+
 def run(n: int = 4096, k: int = 4096, variant: str = "int4gemv_cdna4",
         n_launches: int = 400) -> dict:
     from .sweep import make_sets, window_us
     sets, nbytes = make_sets("int4gemv", n, k, "streaming")
     r = run_stamped(variant, sets, n_launches)
     s = summarize(r["stamps"], r["ticks_per_us"])
+    W0, _, x0, _ = sets[0]
+    from ..ext import Int4gemvExt
+    wpg = int(Int4gemvExt().describe(variant, W0, x0)["block"]) // 64
+    s["by_workgroup"] = by_workgroup(r["stamps"], r["ticks_per_us"], wpg)
     product = window_us("int4gemv", variant, sets, steps=2000, warmup=200)
     return {"variant": variant, "N": n, "K": k, "pool_sets": len(sets),
             "algorithmic_bytes": nbytes, "waves_per_launch": r["waves"],
@@ -130,6 +189,14 @@ def table(rec: dict) -> str:
         lines.append(f"  {p:<22} {v['p50_us']:>12.2f} {v['max_us']:>10.2f}")
     lines.append(f"  span, first wave start .. last y store: {rec['span_us']:.2f}")
     lines.append(f"  gap, last y store .. next launch's first wave start: {rec['gap_us']:.2f}")
+    g = rec.get("by_workgroup")
+    if g:
+        sec = g["barrier_second_on_cu_us"]
+        lines.append(f"  x barrier by workgroup ({g['workgroups']} per launch): first to start "
+                     f"on its CU {g['barrier_first_on_cu_us']:.2f}, second "
+                     + (f"{sec:.2f}" if sec is not None else "-")
+                     + f"; per XCD " + " ".join(f"{v:.2f}" for v in g["barrier_by_xcd_us"])
+                     + f"; corr(start, barrier) {g['corr_start_barrier']:.2f}")
     return "\n".join(lines)
 
 

@@ -519,3 +519,30 @@ def test_window_prefilled_needs_the_wait_to_outlast_the_enqueue_with_margin():
     assert not window_prefilled(0.0, 0.0)                # no wait: never pre-filled
     # the default wait leaves the margin for 20-launch windows at 8 us per launch
     assert window_prefilled(prefill_delay_us(20), 8.0 * 20)
+
+
+def test_timeline_by_workgroup_ranks_workgroups_sharing_a_cu():
+    """Two workgroups of 2 waves on each of 16 CUs: the one that starts later
+    on its CU passes its barrier later; by_workgroup must see it (and the XCD
+    map must invert the kernels' XCD-contiguous block mapping)."""
+    import numpy as np
+    from cudalab_amd.evaluator.timeline import by_workgroup, xcd_of_logical_block
+    assert list(xcd_of_logical_block(16)) == [x for x in range(8) for _ in range(2)]
+    assert list(xcd_of_logical_block(10)) == [0, 0, 1, 1, 2, 3, 4, 5, 6, 7]
+    grid, wpg, tpu = 32, 2, 100.0
+    a = np.zeros((3, grid * wpg, 8), dtype=np.int64)
+    for wg in range(grid):
+        cu, second = wg % 16, wg >= 16
+        for w in range(wpg):
+            row = a[:, wg * wpg + w]
+            row[:, 0] = 1000 + (20 if second else 0) + w          # start: +0.2 us
+            row[:, 1] = 1000 + (150 if second else 90) + 5 * w    # barrier
+            row[:, 5] = cu
+    g = by_workgroup(a, tpu, wpg, skip=0.0)
+    assert g["workgroups"] == grid and g["launches_used"] == 3
+    assert g["barrier_first_on_cu_us"] == pytest.approx(0.95)    # (90 + 5) ticks
+    assert g["barrier_second_on_cu_us"] == pytest.approx(1.55)   # (150 + 5) ticks
+    assert len(g["barrier_by_xcd_us"]) == 8
+    assert g["corr_start_barrier"] > 0.99
+    with pytest.raises(ValueError):
+        by_workgroup(a[:, :63], tpu, wpg)
