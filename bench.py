@@ -529,10 +529,11 @@ def main(argv=None) -> int:
                                        "sets, from a HIP graph: the per-launch cost "
                                        "shared by 8 GEMVs; not the headline caliber")
         if plan.get("kernel") == "lds":
-            from cudalab_amd.evaluator.timeline import run_stamped, summarize
+            from cudalab_amd.evaluator.timeline import by_workgroup, run_stamped, summarize
             tl = run_stamped(args.variant, sets, n_launches=400, warmup=args.warmup,
                              burn_ms=100.0)
             ts = summarize(tl["stamps"], tl["ticks_per_us"])
+            bw = by_workgroup(tl["stamps"], tl["ticks_per_us"], int(plan["block"]) // 64)
             body_span_us = ts["span_us"]
             detail["wave_timeline"] = {
                 "span_us": round(ts["span_us"], 3),
@@ -540,12 +541,21 @@ def main(argv=None) -> int:
                 "points_us": {p: [round(v["p50_us"], 3), round(v["max_us"], 3)]
                               for p, v in ts["points"].items()},
                 "instrumented_us_per_call": round(tl["us_per_launch"], 4),
+                "x_barrier_by_workgroup_us": {
+                    "first_on_cu": round(bw["barrier_first_on_cu_us"], 3),
+                    "second_on_cu": (round(bw["barrier_second_on_cu_us"], 3)
+                                     if bw["barrier_second_on_cu_us"] is not None else None),
+                    "per_xcd": [round(v, 3) for v in bw["barrier_by_xcd_us"]],
+                    "corr_start_barrier": round(bw["corr_start_barrier"], 3)},
                 "note": "cq_int4_timeline over the same pool: a stamped copy of this "
                         "plan's kernel (same arithmetic and launch shape), 400 "
                         "launches; per point [median wave, last wave] in us from "
                         "each launch's first wave start; span = first wave start "
                         "to last y store, gap = last y store to the next launch's "
-                        "first wave start (medians over launches)"}
+                        "first wave start (medians over launches); the x barrier per "
+                        "workgroup: the workgroup that started first on its CU and "
+                        "the second, per XCD, and its correlation with the "
+                        "workgroup's start"}
         gpu_loop("int4gemv", args.variant, sets[:1], nl, args.warmup, 100.0)
         h = windows("int4gemv", args.variant, sets[:1], nl)
         detail["hot_us_per_call"] = round(h["median"], 4)
