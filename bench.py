@@ -390,7 +390,6 @@ def cpu_sweep(seconds: float = 1.0) -> int:
     3) on one input set drawn with the bench recipe (W ~ N(0, 0.02)
     quantized, x ~ N(0, 1)); each result is checked against the oracle's
     bound first.  One JSON line per (op, shape)."""
-    import numpy as np
     import torch
     from oracle import oracle as orc
     from cudalab_amd.int4gemv_quantize import dequantize_w
