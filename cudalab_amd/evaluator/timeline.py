@@ -156,7 +156,14 @@ def by_workgroup(stamps: np.ndarray, ticks_per_us: float, waves_per_group: int,
             "barrier_first_on_cu_us": statistics.median(first),
             "barrier_second_on_cu_us": statistics.median(second) if second else None,
             "barrier_by_xcd_us": per_xcd,
-            "corr_start_barrier": float(np.corrcoef(start.ravel(), barrier.ravel())[0, 1])}
+            "corr_start_barrier": _corr(start.ravel(), barrier.ravel())}
+
+
+def _corr(a: np.ndarray, b: np.ndarray) -> float:
+    """Pearson correlation, NaN when either side is constant."""
+    if a.std() == 0 or b.std() == 0:
+        return float("nan")
+    return float(np.corrcoef(a, b)[0, 1])
 
 
 def run(n: int = 4096, k: int = 4096, variant: str = "int4gemv_cdna4",

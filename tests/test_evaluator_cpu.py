@@ -546,3 +546,17 @@ def test_timeline_by_workgroup_ranks_workgroups_sharing_a_cu():
     assert g["corr_start_barrier"] > 0.99
     with pytest.raises(ValueError):
         by_workgroup(a[:, :63], tpu, wpg)
+
+
+def test_timeline_by_workgroup_constant_starts_give_nan_correlation():
+    import math
+    import numpy as np
+    from cudalab_amd.evaluator.timeline import by_workgroup
+    a = np.zeros((2, 4, 8), dtype=np.int64)
+    a[:, :, 0] = 1000
+    a[:, :, 1] = 1100
+    a[:, :, 5] = np.arange(4)
+    g = by_workgroup(a, 100.0, 1, skip=0.0)
+    assert g["barrier_first_on_cu_us"] == pytest.approx(1.0)
+    assert g["barrier_second_on_cu_us"] is None
+    assert math.isnan(g["corr_start_barrier"])

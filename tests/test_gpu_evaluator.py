@@ -112,7 +112,7 @@ def test_timeline_stamps_every_wave_and_keeps_the_outputs(ext4, N, K):
     threads, two rows per lane on 256, six chunks per lane, a short row."""
     import numpy as np
     import torch
-    from cudalab_amd.evaluator.timeline import run_stamped, summarize
+    from cudalab_amd.evaluator.timeline import by_workgroup, run_stamped, summarize
     from cudalab_amd.operators.int4gemv import device_random_set
     sets = [device_random_set(N, K, 900 + i) for i in range(3)]
     announce(f"timeline {N}x{K}")
@@ -129,6 +129,12 @@ def test_timeline_stamps_every_wave_and_keeps_the_outputs(ext4, N, K):
     assert (starts[1:] >= ends[:-1] - 5).all()    # one stream: launches in order (50 ns slack)
     s = summarize(a, r["ticks_per_us"], skip=0.0)
     assert s["launches_used"] == 5 and 0 < s["span_us"] < 1000
+    g = by_workgroup(a, r["ticks_per_us"], int(d["block"]) // 64, skip=0.0)
+    assert g["workgroups"] == int(d["grid"]) and g["launches_used"] == 6
+    assert 0 < g["barrier_first_on_cu_us"] < 1000
+    if g["barrier_second_on_cu_us"] is not None:      # a CU held two workgroups
+        assert 0 < g["barrier_second_on_cu_us"] < 1000
+    assert 1 <= len(g["barrier_by_xcd_us"]) <= 8
     for W, sc, x, out in sets:
         want = torch.empty_like(out)
         ext4.forward_into("int4gemv_cdna4", W, sc, x, want)
