@@ -125,10 +125,10 @@ def by_workgroup(stamps: np.ndarray, ticks_per_us: float, waves_per_group: int,
     logical-block order.  A workgroup's barrier time is its waves' latest
     x-barrier stamp (they all wait at one barrier), its start their earliest
     start, both from the launch's first wave start.  Workgroups of one launch
-    that share a hardware CU id (stamp word 5) are ranked by start: the
-    report gives the median barrier of the workgroup that started first on
-    its CU and of the second, each XCD's median, and the correlation of a
-    workgroup's start with its barrier."""
+    that share a CU (their XCD and hardware CU id, stamp word 5) are ranked
+    by start: the report gives the median barrier of the workgroup that
+    started first on its CU and of the second, each XCD's median, and the
+    correlation of a workgroup's start with its barrier."""
     L, W, _ = stamps.shape
     if W % waves_per_group:
         raise ValueError("waves per launch not a multiple of the workgroup's waves")
@@ -138,7 +138,11 @@ def by_workgroup(stamps: np.ndarray, ticks_per_us: float, waves_per_group: int,
     rel = (t - t[:, :, 0].min(axis=1)[:, None, None]) / ticks_per_us
     start = rel[:, :, 0].reshape(-1, grid, waves_per_group).min(axis=2)
     barrier = rel[:, :, 1].reshape(-1, grid, waves_per_group).max(axis=2)
-    cu = stamps[lo:, :, 5].reshape(-1, grid, waves_per_group)[:, :, 0]
+    xcd = xcd_of_logical_block(grid)
+    # a CU is keyed by its XCD and its hardware CU id (the id alone need not
+    # distinguish XCDs)
+    cu = (stamps[lo:, :, 5].reshape(-1, grid, waves_per_group)[:, :, 0].astype(np.int64)
+          + (xcd.astype(np.int64) << 32)[None, :])
     first, second = [], []
     for i in range(start.shape[0]):
         order = np.lexsort((start[i], cu[i]))
@@ -149,7 +153,6 @@ def by_workgroup(stamps: np.ndarray, ticks_per_us: float, waves_per_group: int,
         first.append(float(np.median(barrier[i][rank == 0])))
         if (rank == 1).any():
             second.append(float(np.median(barrier[i][rank == 1])))
-    xcd = xcd_of_logical_block(grid)
     per_xcd = [float(np.median(np.median(barrier[:, xcd == x], axis=1)))
                for x in range(8) if (xcd == x).any()]
     return {"workgroups": grid, "launches_used": int(start.shape[0]),

@@ -522,9 +522,11 @@ def test_window_prefilled_needs_the_wait_to_outlast_the_enqueue_with_margin():
 
 
 def test_timeline_by_workgroup_ranks_workgroups_sharing_a_cu():
-    """Two workgroups of 2 waves on each of 16 CUs: the one that starts later
-    on its CU passes its barrier later; by_workgroup must see it (and the XCD
-    map must invert the kernels' XCD-contiguous block mapping)."""
+    """Two workgroups of 2 waves on each of 16 CUs (logical blocks 4x..4x+3
+    run on XCD x; blocks 4x, 4x+2 share one CU and 4x+1, 4x+3 another): the
+    one that starts later on its CU passes its barrier later; by_workgroup
+    must see it, keying a CU by its XCD and hardware id (the XCD map must
+    invert the kernels' XCD-contiguous block mapping)."""
     import numpy as np
     from cudalab_amd.evaluator.timeline import by_workgroup, xcd_of_logical_block
     assert list(xcd_of_logical_block(16)) == [x for x in range(8) for _ in range(2)]
@@ -532,7 +534,7 @@ def test_timeline_by_workgroup_ranks_workgroups_sharing_a_cu():
     grid, wpg, tpu = 32, 2, 100.0
     a = np.zeros((3, grid * wpg, 8), dtype=np.int64)
     for wg in range(grid):
-        cu, second = wg % 16, wg >= 16
+        cu, second = wg % 2, wg % 4 >= 2        # hardware ids repeat across XCDs
         for w in range(wpg):
             row = a[:, wg * wpg + w]
             row[:, 0] = 1000 + (20 if second else 0) + w          # start: +0.2 us
