@@ -28,11 +28,17 @@ pytestmark = pytest.mark.gpu
 INT4_SHAPES = [(1, 128), (3, 128), (16, 256), (65, 384), (300, 1280), (7, 16384),
                (1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096), (4096, 11008),
                (64, 16512), (300, 20480), (4097, 28672), (33, 65536), (2, 131072),
-               (3072, 28672), (3073, 28672)]
+               (3072, 28672), (3073, 28672),
+               # chunks per lane 3, 4, 5, 7 and both sides of the two-rows rule at
+               # short rows (one row per wave up to 8192 waves, two above)
+               (300, 6144), (8192, 8192), (100, 10240), (50, 14336), (8192, 2048),
+               (8193, 2048)]
 Q8_SHAPES = [(1, 1), (16, 13), (8, 7), (17, 16), (300, 1040), (5, 16384),
              (1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096), (4096, 11008),
              (7, 16400), (64, 20480), (4097, 28672), (33, 65536), (2, 131072),
-             (3072, 28672), (3073, 28672)]
+             (3072, 28672), (3073, 28672),
+             # eight chunks per lane on 512-thread workgroups; chunks per lane 3, 5
+             (8192, 8192), (300, 3072), (100, 5120)]
 GEMV_SHAPES = [(1, 1), (16, 13), (33, 1000), (1024, 4096), (4096, 1024), (4096, 4096),
                (11008, 4096), (4096, 11008), (3, 16376), (2, 32768), (300, 40000),
                (33, 65536), (2, 131072)]
