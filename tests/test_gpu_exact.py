@@ -32,7 +32,9 @@ INT4_SHAPES = [(1, 128), (3, 128), (16, 256), (65, 384), (300, 1280), (7, 16384)
                # chunks per lane 3, 4, 5, 7 and both sides of the two-rows rule at
                # short rows (one row per wave up to 8192 waves, two above)
                (300, 6144), (8192, 8192), (100, 10240), (50, 14336), (8192, 2048),
-               (8193, 2048)]
+               (8193, 2048),
+               # the 512-thread forms at 3, 5 and 7 chunks per lane
+               (4096, 6144), (4096, 10240), (4096, 14336)]
 Q8_SHAPES = [(1, 1), (16, 13), (8, 7), (17, 16), (300, 1040), (5, 16384),
              (1024, 4096), (4096, 1024), (4096, 4096), (11008, 4096), (4096, 11008),
              (7, 16400), (64, 20480), (4097, 28672), (33, 65536), (2, 131072),
